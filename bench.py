@@ -1,0 +1,243 @@
+"""Benchmark of the StreamIndex MI355X hot path (BASELINE.json metric).
+
+Default workload = BASELINE config[1]: the V4-Flash indexer on one MI355X,
+B=1, S=65,536, H_I=64, D_I=128, T=16,384, top_k=512, causal_ratio=4,
+chunk_s=2048, chunk_t=8192, seeded bf16/fp32 synthetic inputs resident in HBM.
+One "step" = one ``chunked_indexer_topk`` call (one launch of the fused
+score + top-k kernel).
+
+Printed (one JSON line, rank 0):
+  value          ms per call at S=64K (lower is better)
+  roofline       MFMA bound of the dominant kernel: algorithmic FLOPs
+                 (2·H_I·D_I per causally legal (s,t) pair) / mean kernel time
+                 from HIP events on the launch stream, vs 2516.6 TFLOP/s
+  peak_hbm_gib   max_memory_allocated delta during one call (inputs excluded)
+  parity         recall vs the CPU oracle on sampled rows
+  cpu_baseline   the CPU oracle on a bounded row sample, extrapolated
+  extra          S=1M indexer time (config[4] indexer stage), sparse-attn fwd
+                 at config[3] with its HBM roofline
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from streamindex_amd import chunked_indexer_topk, sparse_attn_fwd, synth  # noqa: E402
+from streamindex_amd import _lib  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+REF_H200_MS = {65536: 122.2, 1048576: 30899.6}  # BASELINE.md §1.1 (H200, not this hardware)
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def _events_time(fn, iters: int, stream: torch.cuda.Stream) -> float:
+    """Mean ms per call, HIP events recorded on `stream` (the launch stream)."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
+
+
+def _peak_gib(fn) -> float:
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = fn()
+    torch.cuda.synchronize()
+    peak = max(0, torch.cuda.max_memory_allocated() - base) / 1024 ** 3
+    del out
+    return peak
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def indexer_parity_and_cpu(q, k, w, idx, sc, ratio, top_k, nrows, seed=0):
+    """Oracle on `nrows` sampled rows: recall + CPU time (the cpu_baseline leg)."""
+    from oracle import oracle as O
+
+    S = q.shape[1]
+    T = k.shape[1]
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(S, size=min(nrows, S), replace=False)).astype(np.int64)
+    qb = _bits(q[0, torch.from_numpy(rows).to(q.device)])
+    kb = _bits(k[0])
+    wb = w[0, torch.from_numpy(rows).to(q.device)].float().cpu().numpy()
+    local = np.arange(len(rows), dtype=np.int64)
+    O.lib()
+    t0 = time.perf_counter()
+    scores = O.indexer_scores(qb, kb, wb, local)  # rows' own q/w are packed densely
+    lim = O.legal_limits(rows, T, ratio)
+    ref_idx, _ = O.topk(scores, lim, top_k)
+    cpu_s = time.perf_counter() - t0
+    got = idx[0].cpu().numpy()[rows]
+    rec = O.set_overlap_recall(ref_idx, got)
+    pairs_sample = float(np.minimum(lim, T).sum())
+    return {
+        "rows": int(len(rows)),
+        "recall_mean": float(rec.mean()),
+        "recall_min": float(rec.min()),
+        "exact_rows_frac": float((rec == 1.0).mean()),
+        "cpu_s": cpu_s,
+        "pairs_sample": pairs_sample,
+    }
+
+
+def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, seed=2026):
+    dev = torch.device("cuda:0")
+    q, k, w = synth.indexer_inputs(1, S, H, D, ratio=ratio, seed=seed, device=dev)
+    T = k.shape[1]
+    fn = lambda: chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=chunk_s, chunk_t=chunk_t)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        out = fn()
+    torch.cuda.synchronize()
+    peak = _peak_gib(fn)
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = _events_time(fn, steps, stream)
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    flops = synth.indexer_flops(S, T, H, D, ratio)
+    idx, sc = fn()
+    torch.cuda.synchronize()
+    return dict(q=q, k=k, w=w, T=T, ms=ms, wall_ms=wall, peak_gib=peak, flops=flops, idx=idx, sc=sc)
+
+
+def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None):
+    dev = torch.device("cuda:0")
+    q, kv, sink = synth.sparse_attn_inputs(1, S, H, D, T, seed=2027, device=dev)
+    if idx is None:
+        idx = synth.causal_random_topk(1, S, top_k, 4, device=dev)
+    fn = lambda: sparse_attn_fwd(q, kv, sink, idx, D ** -0.5)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
+    nvalid = float((idx >= 0).sum().item())
+    flops = 4.0 * H * D * nvalid
+    unique_bytes = (q.numel() * 2 * 2 + idx.numel() * idx.element_size() + S * H * 4 + kv.numel() * 2)
+    return dict(ms=ms, flops=flops, unique_bytes=unique_bytes, nvalid=nvalid)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--seq", type=int, default=65536)
+    ap.add_argument("--top-k", type=int, default=512)
+    ap.add_argument("--ratio", type=int, default=4)
+    ap.add_argument("--chunk-s", type=int, default=2048)
+    ap.add_argument("--chunk-t", type=int, default=8192)
+    ap.add_argument("--parity-rows", type=int, default=4096)
+    ap.add_argument("--no-long", action="store_true", help="skip the S=1M indexer measurement")
+    ap.add_argument("--no-attn", action="store_true", help="skip the sparse-attention measurement")
+    ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}), flush=True)
+        sys.exit(1)
+    _lib.load()
+
+    print(f"[bench] indexer S={args.seq} warmup={args.warmup} steps={args.steps}", file=sys.stderr, flush=True)
+    r = run_indexer(args.seq, args.ratio, args.top_k, args.chunk_s, args.chunk_t, args.steps, args.warmup)
+    if args.only_indexer:
+        print(json.dumps({"indexer_ms": r["ms"], "tflops": r["flops"] / r["ms"] / 1e9}), flush=True)
+        return
+    tflops = r["flops"] / (r["ms"] * 1e-3) / 1e12
+    print(f"[bench] indexer {r['ms']:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    print(f"[bench] parity + cpu baseline on {args.parity_rows} sampled rows", file=sys.stderr, flush=True)
+    par = indexer_parity_and_cpu(r["q"], r["k"], r["w"], r["idx"], r["sc"], args.ratio, args.top_k,
+                                 args.parity_rows)
+    total_pairs = synth.legal_pairs(args.seq, r["T"], args.ratio)
+    cpu_ms_full = par["cpu_s"] * 1e3 * total_pairs / max(1.0, par["pairs_sample"])
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    del r["q"], r["k"], r["w"], r["idx"], r["sc"]
+    torch.cuda.empty_cache()
+
+    extra = {"indexer_wall_ms_per_call": r["wall_ms"], "reference_h200_ms_s64k": REF_H200_MS[65536]}
+    if not args.no_long:
+        print("[bench] indexer S=1M (config[4] indexer stage)", file=sys.stderr, flush=True)
+        rl = run_indexer(1 << 20, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
+        extra["s1m_ms"] = rl["ms"]
+        extra["s1m_tflops"] = rl["flops"] / (rl["ms"] * 1e-3) / 1e12
+        extra["s1m_peak_hbm_gib"] = rl["peak_gib"]
+        extra["reference_h200_ms_s1m"] = REF_H200_MS[1048576]
+        del rl
+        torch.cuda.empty_cache()
+    if not args.no_attn:
+        print("[bench] sparse attention config[3]", file=sys.stderr, flush=True)
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1)
+        extra["sparse_attn_ms"] = ra["ms"]
+        extra["sparse_attn_tflops"] = ra["flops"] / (ra["ms"] * 1e-3) / 1e12
+        extra["sparse_attn_unique_gbps"] = ra["unique_bytes"] / (ra["ms"] * 1e-3) / 1e9
+        extra["sparse_attn_hbm_frac"] = extra["sparse_attn_unique_gbps"] / PEAK_HBM_GBPS
+        extra["sparse_attn_mfma_frac"] = extra["sparse_attn_tflops"] / PEAK_BF16_TFLOPS
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        try:
+            with open(TRAFFIC_FILE) as f:
+                traffic = json.load(f).get("indexer_topk_c1_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    line = {
+        "metric": "V4-Flash indexer ms @S=64K/1M, MFMA util %, peak HBM GB (1 GPU)",
+        "value": round(r["ms"], 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)-scaled, BASELINE config[1])",
+        "config": {"workload": "v4_flash_indexer_c1", "B": 1, "S": args.seq, "T": args.seq // args.ratio,
+                   "H_I": 64, "D_I": 128, "top_k": args.top_k, "causal_ratio": args.ratio,
+                   "chunk_s": args.chunk_s, "chunk_t": args.chunk_t},
+        "mfma_util_pct": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "peak_hbm_gib": round(r["peak_gib"], 4),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "kernel": "indexer_topk_kernel", "flops_per_launch": r["flops"]},
+        "parity": {k: par[k] for k in ("rows", "recall_mean", "recall_min", "exact_rows_frac")},
+        "cpu_baseline": {"value": round(cpu_ms_full, 1), "unit": "ms (extrapolated to the full S=64K job)",
+                         "cores": threads, "kind": "port",
+                         "sample": f"{par['rows']} sampled query rows of config[1] through the C oracle "
+                                   f"(scores in double + top-k), {par['cpu_s']:.2f} s measured, scaled by "
+                                   f"legal (s,t) pairs"},
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

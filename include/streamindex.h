@@ -1,0 +1,99 @@
+/*
+ * StreamIndex for MI355X — C ABI of libstreamindex.so.
+ *
+ * Plain pointers, element strides and sizes; no torch or HIP C++ types.  All
+ * device pointers are HIP device memory; `stream` is a hipStream_t passed as
+ * void* (NULL = the default stream).  Every call is asynchronous on `stream`,
+ * allocates nothing, and returns a status code:
+ *
+ *   0 SI_OK, 1 SI_ERR_INVALID (bad argument), 2 SI_ERR_UNSUPPORTED (valid but
+ *   outside the implemented shapes), 3 SI_ERR_LAUNCH (HIP launch error).
+ *
+ * On a non-zero status si_last_error() returns a thread-local description.
+ *
+ * The reference (tsukimia-hoshi/StreamIndex) is Python + Triton with no C
+ * FFI; each entry below replaces one of its Python operators, cited by
+ * file:line in the reference tree.  The Python binding that mirrors those
+ * operators is streamindex_amd/_lib.py (ctypes).
+ */
+#ifndef STREAMINDEX_H_
+#define STREAMINDEX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SI_OK 0
+#define SI_ERR_INVALID 1
+#define SI_ERR_UNSUPPORTED 2
+#define SI_ERR_LAUNCH 3
+
+/* Version of this interface (incremented on any signature change). */
+int si_abi_version(void);
+
+/* Thread-local text of the last error returned on this thread. */
+const char* si_last_error(void);
+
+/*
+ * Device workspace si_indexer_topk needs (always 0: selection state lives in
+ * LDS).  Replaces the chunk_s x chunk_t fp32 score tile the reference driver
+ * allocates per (s-chunk, t-chunk) pair,
+ * flash_sparse/triton/chunked_indexer.py:92-118.
+ */
+size_t si_indexer_topk_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                                       int64_t top_k);
+
+/*
+ * Fused lightning-indexer score + exact top-k per query row.
+ * Replaces flash_sparse/triton/chunked_indexer.py:47-160 (chunked_indexer_topk)
+ * and, with out width min(top_k,T), indexer_score.py:182-205 (indexer_score_topk).
+ *
+ *   q        [B,S,H,D] bf16, strides q_strides[4] (elements; last must be 1)
+ *   k_idx    [B,T,D]   bf16, strides k_strides[3] (last must be 1)
+ *   weights  [B,S,H]   fp32 (w_dtype 0) or bf16 (w_dtype 1), strides w_strides[3]
+ *   mask     optional [B,S,T] bool (1 byte, nonzero = legal), strides mask_strides[3]; NULL = none
+ *   causal_ratio > 0: key t legal for row s iff t < (s+1)/causal_ratio; 0 = none.
+ *                     Must be 0 when mask != NULL.
+ *   out_idx    [B,S,top_k] int64, contiguous: best-first, -1 past the legal count
+ *   out_scores [B,S,top_k] fp32,  contiguous: best-first, -inf past the legal count
+ * Ties rank the smaller key index first.  Supported: H <= 64, D in {32,64,128},
+ * 1 <= top_k <= 2048.
+ */
+int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, const int64_t* k_strides,
+                    const void* weights, int w_dtype, const int64_t* w_strides, const uint8_t* mask,
+                    const int64_t* mask_strides, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                    int64_t top_k, int64_t causal_ratio, int64_t* out_idx, float* out_scores, void* stream);
+
+/*
+ * Materialised indexer score matrix scores[b,s,t] = sum_h w[b,s,h]*relu(q[b,s,h,:].k[b,t,:]),
+ * fp32 with strides score_strides[3].  No mask.
+ * Replaces flash_sparse/triton/indexer_score.py:41-179 (_indexer_score_kernel, indexer_score).
+ */
+int si_indexer_score(const void* q, const int64_t* q_strides, const void* k_idx, const int64_t* k_strides,
+                     const void* weights, int w_dtype, const int64_t* w_strides, int64_t B, int64_t S,
+                     int64_t T, int64_t H, int64_t D, float* scores, const int64_t* score_strides,
+                     void* stream);
+
+/*
+ * MQA sparse attention forward with attention sink.
+ * Replaces flash_sparse/triton/sparse_attn_fwd.py:40-292 (_sparse_attn_fwd_kernel, sparse_attn_fwd).
+ *
+ *   q [B,S,H,D] bf16; kv [B,N_kv,D] bf16; attn_sink [H] fp32;
+ *   topk_idxs [B,S,K] int32 (idx_is_i64 = 0) or int64 (1); -1 or >= N_kv = masked.
+ *   o [B,S,H,D] bf16 out; lse [B,S,H] fp32 out (natural log, sink included).
+ * Supported: H <= 128, D in {32,64,128,256,512,576}.
+ */
+int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                       const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                       const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D, int64_t N_kv,
+                       int64_t K, float softmax_scale, void* o, const int64_t* o_strides, float* lse,
+                       const int64_t* lse_strides, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STREAMINDEX_H_ */

@@ -1,0 +1,284 @@
+"""CPU oracle for the StreamIndex CSA hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` import this module, and only as the checker.  The product
+(``streamindex_amd``) never imports, loads or calls anything here.
+
+Two independent restatements of the reference's materialise-then-topk path
+live here:
+
+* the C oracle in ``si_oracle.c`` (double accumulation, OpenMP), used for
+  anything larger than a toy, bound through ctypes below;
+* small numpy versions (``np_*``) used to cross-check the C code on tiny
+  shapes, together with brute-force and closed-form checks in
+  ``tests/test_oracle.py``.
+
+Reference semantics followed (file:line in the reference tree):
+
+* score: ``flash_sparse/reference.py:138-168`` (eq. 16);
+* mask / topk / post-mask: ``eval/test_v4_indexer_parity.py:111-137``;
+* chunked output width ``top_k`` with ``-1`` / ``-inf`` padding:
+  ``flash_sparse/triton/chunked_indexer.py:89-110,154-158``;
+* tie order (score desc, index asc): ``docs/streaming_topk.md:46-60``;
+* set-overlap recall: ``eval/test_v4_indexer_parity.py:164-199``;
+* sparse attention with sink: ``flash_sparse/reference.py:44-130``;
+  LSE: ``flash_sparse/triton/sparse_attn_fwd.py:148-177``.
+
+Parity status: every function here is pinned by ``tests/test_oracle.py``
+(brute force on tiny inputs, closed forms, invariants, and torch's own CPU
+``einsum``/``topk``/``softmax`` as an independent library implementation).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compiles ``liboracle.so`` with the committed Makefile (gcc, OpenMP)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-C", _HERE, "-B" if force else "liboracle.so"], check=True,
+                       stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I = ctypes.c_int64
+        L.oracle_indexer_scores.argtypes = [P, P, P, I, I, I, I, P, I, P]
+        L.oracle_indexer_scores.restype = None
+        L.oracle_indexer_scores_f32.argtypes = [P, P, P, I, I, I, I, P, I, P]
+        L.oracle_indexer_scores_f32.restype = None
+        L.oracle_topk.argtypes = [P, I, I, P, P, I, P, P]
+        L.oracle_topk.restype = None
+        L.oracle_sparse_attn.argtypes = [P, P, P, P, I, I, I, I, I, ctypes.c_double, P, P]
+        L.oracle_sparse_attn.restype = None
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers (inputs are carried as raw uint16 bit patterns)
+# ---------------------------------------------------------------------------
+def bf16_bits_to_f64(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return rounded.astype(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# Indexer (C oracle)
+# ---------------------------------------------------------------------------
+def indexer_scores(q_bits: np.ndarray, k_bits: np.ndarray, w: np.ndarray, rows: Optional[np.ndarray] = None,
+                   precision: str = "f64") -> np.ndarray:
+    """Scores ``I(s, t)`` for the selected query rows of ONE batch.
+
+    q_bits [S,H,D] uint16 (bf16 bits), k_bits [T,D] uint16, w [S,H] float32.
+    Returns [len(rows), T] float64 (or float32 with ``precision='f32'``).
+    """
+    S, H, D = q_bits.shape
+    T = k_bits.shape[0]
+    q_bits = np.ascontiguousarray(q_bits, dtype=np.uint16)
+    k_bits = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows = np.arange(S, dtype=np.int64) if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    if precision == "f64":
+        out = np.empty((len(rows), T), dtype=np.float64)
+        lib().oracle_indexer_scores(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows), len(rows),
+                                    _ptr(out))
+    else:
+        out = np.empty((len(rows), T), dtype=np.float32)
+        lib().oracle_indexer_scores_f32(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows), len(rows),
+                                        _ptr(out))
+    return out
+
+
+def legal_limits(rows: np.ndarray, T: int, causal_ratio: Optional[int]) -> np.ndarray:
+    """Number of legal leading keys per row: ``min(T, (s+1)//ratio)`` or ``T``."""
+    rows = np.asarray(rows, dtype=np.int64)
+    if causal_ratio is None:
+        return np.full(rows.shape, T, dtype=np.int64)
+    return np.minimum(T, (rows + 1) // int(causal_ratio)).astype(np.int64)
+
+
+def topk(scores: np.ndarray, lim: np.ndarray, top_k: int, mask: Optional[np.ndarray] = None):
+    """Per-row top-k (score desc, index asc) over legal keys, width ``top_k``."""
+    scores = np.ascontiguousarray(scores, dtype=np.float64)
+    n, T = scores.shape
+    lim = np.ascontiguousarray(lim, dtype=np.int64)
+    idx = np.empty((n, top_k), dtype=np.int64)
+    val = np.empty((n, top_k), dtype=np.float64)
+    mptr = None
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.uint8)
+        mptr = _ptr(mask)
+    lib().oracle_topk(_ptr(scores), n, T, _ptr(lim), mptr, top_k, _ptr(idx), _ptr(val))
+    return idx, val
+
+
+def indexer_topk_rows(q_bits, k_bits, w, top_k: int, *, rows=None, causal_ratio=None, mask_rows=None):
+    """Materialise-then-topk for the selected rows of one batch.
+
+    Returns (idx [n,top_k] int64, score [n,top_k] float64, scores [n,T] float64).
+    """
+    S = q_bits.shape[0]
+    T = k_bits.shape[0]
+    rows = np.arange(S, dtype=np.int64) if rows is None else np.asarray(rows, dtype=np.int64)
+    sc = indexer_scores(q_bits, k_bits, w, rows)
+    lim = legal_limits(rows, T, causal_ratio)
+    idx, val = topk(sc, lim, top_k, mask_rows)
+    return idx, val, sc
+
+
+# ---------------------------------------------------------------------------
+# Sparse attention (C oracle)
+# ---------------------------------------------------------------------------
+def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float):
+    """Reference sparse attention for ``n`` rows of one batch.
+
+    q_bits [n,H,D] uint16, kv_bits [N,D] uint16, sink [H] f32, idx [n,K] int.
+    Returns (o [n,H,D] float64, lse [n,H] float64).
+    """
+    n, H, D = q_bits.shape
+    N = kv_bits.shape[0]
+    K = idx.shape[1]
+    q_bits = np.ascontiguousarray(q_bits, dtype=np.uint16)
+    kv_bits = np.ascontiguousarray(kv_bits, dtype=np.uint16)
+    sink = np.ascontiguousarray(sink, dtype=np.float32)
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    o = np.empty((n, H, D), dtype=np.float64)
+    lse = np.empty((n, H), dtype=np.float64)
+    lib().oracle_sparse_attn(_ptr(q_bits), _ptr(kv_bits), _ptr(sink), _ptr(idx), n, H, D, N, K, float(scale),
+                             _ptr(o), _ptr(lse))
+    return o, lse
+
+
+# ---------------------------------------------------------------------------
+# numpy restatements (tiny shapes only; cross-checks of the C oracle)
+# ---------------------------------------------------------------------------
+def np_indexer_scores(qf: np.ndarray, kf: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """qf [S,H,D], kf [T,D], w [S,H] (float64) -> [S,T]; reference.py:165-168."""
+    qk = np.einsum("shd,td->sht", qf, kf)
+    return (np.maximum(qk, 0.0) * w[:, :, None]).sum(axis=1)
+
+
+def np_topk(scores: np.ndarray, lim: np.ndarray, top_k: int) -> tuple:
+    """Lexicographic (score desc, index asc) selection with -1/-inf padding."""
+    n, T = scores.shape
+    idx = np.full((n, top_k), -1, dtype=np.int64)
+    val = np.full((n, top_k), -np.inf)
+    for r in range(n):
+        L = int(min(T, lim[r]))
+        t = np.arange(L)
+        order = np.lexsort((t, -scores[r, :L]))[:top_k]
+        idx[r, : len(order)] = t[order]
+        val[r, : len(order)] = scores[r, order]
+    return idx, val
+
+
+def np_chunked_topk(scores: np.ndarray, lim: np.ndarray, top_k: int, chunk_t: int) -> tuple:
+    """Partition-merge restatement of chunked_indexer.py:112-155 on a score row
+    block: per-chunk top-min(k,cT) then merge into a running top-k."""
+    n, T = scores.shape
+    run_i = np.full((n, top_k), -1, dtype=np.int64)
+    run_v = np.full((n, top_k), -np.inf)
+    for t0 in range(0, T, chunk_t):
+        t1 = min(t0 + chunk_t, T)
+        blk = scores[:, t0:t1].copy()
+        tt = np.arange(t0, t1)
+        blk[tt[None, :] >= lim[:, None]] = -np.inf
+        kc = min(top_k, t1 - t0)
+        ci = np.empty((n, kc), dtype=np.int64)
+        cv = np.empty((n, kc))
+        for r in range(n):
+            o = np.lexsort((tt, -blk[r]))[:kc]
+            ci[r] = tt[o]
+            cv[r] = blk[r, o]
+        ci = np.where(np.isinf(cv), -1, ci)
+        allv = np.concatenate([run_v, cv], axis=1)
+        alli = np.concatenate([run_i, ci], axis=1)
+        for r in range(n):
+            # -1 sorts after every real index among -inf ties
+            key_i = np.where(alli[r] < 0, np.iinfo(np.int64).max, alli[r])
+            o = np.lexsort((key_i, -allv[r]))[:top_k]
+            run_v[r] = allv[r, o]
+            run_i[r] = alli[r, o]
+        run_i = np.where(np.isinf(run_v), -1, run_i)
+    return run_i, run_v
+
+
+def np_sparse_attn(qf: np.ndarray, kvf: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float):
+    """qf [n,H,D], kvf [N,D], sink [H], idx [n,K] -> (o [n,H,D], lse [n,H]); reference.py:93-130."""
+    n, H, D = qf.shape
+    valid = idx >= 0
+    g = kvf[np.where(valid, idx, 0)] * valid[..., None]           # [n,K,D]
+    sc = np.einsum("nhd,nkd->nhk", qf, g) * scale
+    sc = np.where(valid[:, None, :], sc, -np.inf)
+    mx = np.maximum(sc.max(axis=-1), sink[None, :])                 # [n,H]
+    p = np.exp(sc - mx[..., None])
+    den = p.sum(-1) + np.exp(sink[None, :] - mx)
+    o = np.einsum("nhk,nkd->nhd", p, g) / den[..., None]
+    lse = np.log(den) + mx
+    return o, lse
+
+
+# ---------------------------------------------------------------------------
+# Metrics
+# ---------------------------------------------------------------------------
+def set_overlap_recall(idx_a: np.ndarray, idx_b: np.ndarray) -> np.ndarray:
+    """Per-row |valid_a ∩ valid_b| / |valid_a| (eval/test_v4_indexer_parity.py:164-199).
+
+    Negative entries are padding.  Both empty -> 1; a empty, b non-empty -> 0.
+    Accepts [..., K] arrays; returns [...] float64.
+    """
+    a = np.asarray(idx_a, dtype=np.int64)
+    b = np.asarray(idx_b, dtype=np.int64)
+    lead = a.shape[:-1]
+    a2 = a.reshape(-1, a.shape[-1])
+    b2 = b.reshape(-1, b.shape[-1])
+    out = np.empty(a2.shape[0])
+    for r in range(a2.shape[0]):
+        va = set(int(x) for x in a2[r] if x >= 0)
+        vb = set(int(x) for x in b2[r] if x >= 0)
+        if not va:
+            out[r] = 1.0 if not vb else 0.0
+        else:
+            out[r] = len(va & vb) / len(va)
+    return out.reshape(lead)
+
+
+def boundary_gap(ref_scores_sorted: np.ndarray, all_scores: np.ndarray, lim: np.ndarray, top_k: int) -> np.ndarray:
+    """Gap between the k-th and (k+1)-th best legal score per row (inf when the
+    row has at most k legal keys)."""
+    n = all_scores.shape[0]
+    gap = np.full(n, np.inf)
+    for r in range(n):
+        L = int(lim[r])
+        if L <= top_k:
+            continue
+        row = np.sort(all_scores[r, :L])[::-1]
+        gap[r] = row[top_k - 1] - row[top_k]
+    return gap

@@ -1,0 +1,208 @@
+/*
+ * CPU oracle for the StreamIndex CSA hot path.  TEST INFRASTRUCTURE ONLY:
+ * this file is the checker that tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py compare the HIP kernels against.  No product
+ * code path links, loads or calls it.
+ *
+ * It restates, from scratch, the reference's materialise-then-topk path:
+ *   score      flash_sparse/reference.py:138-168   (eq. 16, fp32 einsum -> relu -> w-sum)
+ *   mask/topk  eval/test_v4_indexer_parity.py:111-137 (illegal t >= (s+1)//ratio -> -inf,
+ *              topk(min(k,T)), post-mask -> -1)
+ *   tie order  docs/streaming_topk.md:46-60,301-312 (score desc, index asc)
+ *   attention  flash_sparse/reference.py:44-130 (gather, sink-augmented softmax)
+ *              flash_sparse/triton/sparse_attn_fwd.py:148-177 (LSE, -1e30 when empty)
+ *
+ * Arithmetic: bf16 inputs are widened exactly; every dot product and every
+ * head/key sum is accumulated in double, which is at least as accurate as the
+ * reference's fp32 einsum and gives the "true" value the kernels are judged
+ * against.  A float-accumulation variant of the score mirrors the reference's
+ * working precision for gap diagnostics.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = ((uint32_t)b) << 16;
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+/*
+ * Scores of `nrows` query rows against all T keys (one batch).
+ *   q   [S, H, D] bf16 bits       k [T, D] bf16 bits       w [S, H] fp32
+ *   rows[i] selects the query row; out [nrows, T] (double).
+ * Follows reference.py:165-168: relu per head, then the weighted head sum.
+ */
+void oracle_indexer_scores(const uint16_t* q, const uint16_t* k, const float* w, int64_t S, int64_t T,
+                           int64_t H, int64_t D, const int64_t* rows, int64_t nrows, double* out) {
+  (void)S;
+  double* kd = (double*)malloc(sizeof(double) * (size_t)(T * D));
+  for (int64_t i = 0; i < T * D; ++i) kd[i] = (double)bf16_to_f32(k[i]);
+#pragma omp parallel
+  {
+    double* qd = (double*)malloc(sizeof(double) * (size_t)(H * D));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t r = 0; r < nrows; ++r) {
+      const int64_t s = rows[r];
+      for (int64_t i = 0; i < H * D; ++i) qd[i] = (double)bf16_to_f32(q[s * H * D + i]);
+      const float* ws = w + s * H;
+      for (int64_t t = 0; t < T; ++t) {
+        const double* kt = kd + t * D;
+        double acc = 0.0;
+        for (int64_t h = 0; h < H; ++h) {
+          const double* qh = qd + h * D;
+          double dot = 0.0;
+          for (int64_t d = 0; d < D; ++d) dot += qh[d] * kt[d];
+          if (dot > 0.0) acc += (double)ws[h] * dot;
+        }
+        out[r * T + t] = acc;
+      }
+    }
+    free(qd);
+  }
+  free(kd);
+}
+
+/* Same as above in float accumulation (the reference's working precision). */
+void oracle_indexer_scores_f32(const uint16_t* q, const uint16_t* k, const float* w, int64_t S, int64_t T,
+                               int64_t H, int64_t D, const int64_t* rows, int64_t nrows, float* out) {
+  (void)S;
+  float* kf = (float*)malloc(sizeof(float) * (size_t)(T * D));
+  for (int64_t i = 0; i < T * D; ++i) kf[i] = bf16_to_f32(k[i]);
+#pragma omp parallel
+  {
+    float* qf = (float*)malloc(sizeof(float) * (size_t)(H * D));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t r = 0; r < nrows; ++r) {
+      const int64_t s = rows[r];
+      for (int64_t i = 0; i < H * D; ++i) qf[i] = bf16_to_f32(q[s * H * D + i]);
+      const float* ws = w + s * H;
+      for (int64_t t = 0; t < T; ++t) {
+        const float* kt = kf + t * D;
+        float acc = 0.0f;
+        for (int64_t h = 0; h < H; ++h) {
+          const float* qh = qf + h * D;
+          float dot = 0.0f;
+          for (int64_t d = 0; d < D; ++d) dot += qh[d] * kt[d];
+          acc += ws[h] * (dot > 0.0f ? dot : 0.0f);
+        }
+        out[r * T + t] = acc;
+      }
+    }
+    free(qf);
+  }
+  free(kf);
+}
+
+typedef struct {
+  double v;
+  int64_t i;
+} si_pair;
+
+/* (score desc, index asc): docs/streaming_topk.md:46-60. */
+static int cmp_pair(const void* a, const void* b) {
+  const si_pair* x = (const si_pair*)a;
+  const si_pair* y = (const si_pair*)b;
+  if (x->v > y->v) return -1;
+  if (x->v < y->v) return 1;
+  return (x->i < y->i) ? -1 : (x->i > y->i);
+}
+
+/*
+ * Per-row top-k over legal keys.
+ *   scores [nrows, T]; legal key t of row r: t < lim[r] and (mask == NULL or mask[r*T+t]).
+ *   Output width top_k; positions past the number of legal keys get index -1
+ *   and score -inf (eval/test_v4_indexer_parity.py:124-136 and the chunked
+ *   driver's isinf -> -1 rule, chunked_indexer.py:154-155).
+ */
+void oracle_topk(const double* scores, int64_t nrows, int64_t T, const int64_t* lim, const uint8_t* mask,
+                 int64_t top_k, int64_t* out_idx, double* out_score) {
+#pragma omp parallel
+  {
+    si_pair* buf = (si_pair*)malloc(sizeof(si_pair) * (size_t)(T > 0 ? T : 1));
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t r = 0; r < nrows; ++r) {
+      int64_t n = 0;
+      const int64_t L = lim[r] < T ? lim[r] : T;
+      for (int64_t t = 0; t < L; ++t) {
+        if (mask && !mask[r * T + t]) continue;
+        buf[n].v = scores[r * T + t];
+        buf[n].i = t;
+        ++n;
+      }
+      qsort(buf, (size_t)n, sizeof(si_pair), cmp_pair);
+      for (int64_t j = 0; j < top_k; ++j) {
+        if (j < n) {
+          out_idx[r * top_k + j] = buf[j].i;
+          out_score[r * top_k + j] = buf[j].v;
+        } else {
+          out_idx[r * top_k + j] = -1;
+          out_score[r * top_k + j] = -INFINITY;
+        }
+      }
+    }
+    free(buf);
+  }
+}
+
+/*
+ * Sparse attention with attention sink, MQA layout (reference.py:93-130), for
+ * `nrows` query rows of one batch.
+ *   q [nrows, H, D] bf16 bits; kv [N, D] bf16 bits; sink [H] fp32;
+ *   idx [nrows, K] int64 (-1 = masked).  Out: o [nrows, H, D], lse [nrows, H].
+ * The sink enters the denominator only.  LSE = log(sum) + max as in
+ * sparse_attn_fwd.py:174-177 (sink included in the sum).
+ */
+void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink, const int64_t* idx,
+                        int64_t nrows, int64_t H, int64_t D, int64_t N, int64_t K, double scale,
+                        double* o, double* lse) {
+#pragma omp parallel
+  {
+    double* sc = (double*)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+    double* qd = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t r = 0; r < nrows; ++r) {
+      const int64_t* ir = idx + r * K;
+      for (int64_t h = 0; h < H; ++h) {
+        const uint16_t* qh = q + (r * H + h) * D;
+        for (int64_t d = 0; d < D; ++d) qd[d] = (double)bf16_to_f32(qh[d]);
+        double mx = (double)sink[h];
+        for (int64_t j = 0; j < K; ++j) {
+          const int64_t t = ir[j];
+          if (t < 0 || t >= N) {
+            sc[j] = -INFINITY;
+            continue;
+          }
+          const uint16_t* kr = kv + t * D;
+          double dot = 0.0;
+          for (int64_t d = 0; d < D; ++d) dot += qd[d] * (double)bf16_to_f32(kr[d]);
+          sc[j] = dot * scale;
+          if (sc[j] > mx) mx = sc[j];
+        }
+        double* oh = o + (r * H + h) * D;
+        for (int64_t d = 0; d < D; ++d) oh[d] = 0.0;
+        if (mx == -INFINITY) {
+          /* No valid key and a -inf sink: zero output and the kernel's
+           * "empty" LSE sentinel (sparse_attn_fwd.py:159-161,174-175). */
+          lse[r * H + h] = -1.0e30;
+          continue;
+        }
+        double den = exp((double)sink[h] - mx);
+        for (int64_t j = 0; j < K; ++j) {
+          if (sc[j] == -INFINITY) continue;
+          const double p = exp(sc[j] - mx);
+          den += p;
+          const uint16_t* kr = kv + ir[j] * D;
+          for (int64_t d = 0; d < D; ++d) oh[d] += p * (double)bf16_to_f32(kr[d]);
+        }
+        for (int64_t d = 0; d < D; ++d) oh[d] /= den;
+        lse[r * H + h] = log(den) + mx;
+      }
+    }
+    free(sc);
+    free(qd);
+  }
+}

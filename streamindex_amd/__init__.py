@@ -1,0 +1,25 @@
+"""StreamIndex for MI355X: the DeepSeek-V4 CSA hot path on gfx950.
+
+Operators (hand-written HIP kernels behind the C ABI in
+``include/streamindex.h``, loaded from ``streamindex_amd/lib/libstreamindex.so``):
+
+* :func:`chunked_indexer_topk` — fused lightning-indexer score + exact top-k;
+* :func:`indexer_score`, :func:`indexer_score_topk`;
+* :func:`sparse_attn_fwd`, :func:`sparse_attn` — MQA sparse attention with sink.
+
+The same names are importable under the reference's module paths through the
+``flash_sparse`` package (``flash_sparse.triton.chunked_indexer`` etc.).
+"""
+
+from .indexer import chunked_indexer_topk, indexer_score, indexer_score_topk
+from .sparse_attn import sparse_attn, sparse_attn_fwd
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "chunked_indexer_topk",
+    "indexer_score",
+    "indexer_score_topk",
+    "sparse_attn",
+    "sparse_attn_fwd",
+]

@@ -1,0 +1,82 @@
+// Shared device helpers for the StreamIndex gfx950 kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts,
+// v_mfma_f32_{32x32x16,16x16x32}_bf16 matrix cores and 160 KiB of LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace si {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Order-preserving float <-> uint32 map.  ord(a) > ord(b) as unsigned integers
+// iff a > b as floats (for all non-NaN values; -0.0 is folded onto +0.0 first
+// so that the two zeros tie, as they do under IEEE comparison).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_to_ord(float x) {
+  x = x + 0.0f;  // -0.0 + 0.0 == +0.0 under round-to-nearest
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float ord_to_f32(uint32_t o) {
+  const uint32_t b = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+  return __uint_as_float(b);
+}
+
+// A selection key packs (score, index) so that a larger unsigned 64-bit key
+// means "ranks higher" under the total order used by the indexer top-k:
+// higher score first, and on equal score the smaller index first.  The key 0
+// is the empty-slot sentinel; every real key is larger because ord() of a
+// finite float is at least 0x00800000.
+__device__ __forceinline__ uint64_t make_key(float score, uint32_t idx) {
+  return (static_cast<uint64_t>(f32_to_ord(score)) << 32) | static_cast<uint64_t>(~idx);
+}
+__device__ __forceinline__ uint32_t key_hi(uint64_t k) { return static_cast<uint32_t>(k >> 32); }
+__device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~static_cast<uint32_t>(k); }
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers (ds_bpermute based; works for any xor mask in a wave64).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int lane, int mask) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, static_cast<int>(v)));
+}
+__device__ __forceinline__ float shfl_xor_f32(float v, int lane, int mask) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int mask) {
+  const uint32_t lo = shfl_xor_u32(static_cast<uint32_t>(v), lane, mask);
+  const uint32_t hi = shfl_xor_u32(static_cast<uint32_t>(v >> 32), lane, mask);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+
+// Number of set bits of `m` in lanes strictly below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+}
+
+// Orders this wave's LDS traffic: every LDS write issued before the call is
+// visible to every lane of the same wave after it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+}  // namespace si

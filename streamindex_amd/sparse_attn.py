@@ -1,0 +1,113 @@
+"""Sparse-attention forward on MI355X (gfx950 HIP kernel via the C ABI).
+
+Mirrors ``flash_sparse/triton/sparse_attn_fwd.py:180-292`` (``sparse_attn_fwd``)
+and the forward half of ``flash_sparse/triton/__init__.py:19-60``
+(``sparse_attn``).  Same argument names, shapes, dtypes and return values.
+
+Differences, all deliberate:
+
+* ``D`` may be any of 32, 64, 128, 256, 512 or 576 — including the V4 head dim
+  576 that the reference kernel rejects (``sparse_attn_fwd.py:217-218``).
+* ``block_h`` / ``block_n`` are accepted and ignored: the kernel gathers each
+  query's KV rows once for all heads, so there is no head-block knob.
+* An index ``>= N_kv`` is treated like ``-1`` (masked) instead of reading out
+  of bounds.
+* ``sparse_attn`` is forward-only: calling ``backward`` raises.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+SUPPORTED_D = (32, 64, 128, 256, 512, 576)
+MAX_HEADS = 128
+
+
+def sparse_attn_fwd(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    attn_sink: torch.Tensor,
+    topk_idxs: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    *,
+    block_h: Optional[int] = None,
+    block_n: int = 64,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """MQA sparse attention with attention sink.
+
+    Args:
+      q: ``[B, S, H, D]`` bf16.  kv: ``[B, N_kv, D]`` bf16 (one shared head).
+      attn_sink: ``[H]`` fp32.  topk_idxs: ``[B, S, K]`` int32/int64, ``-1`` = masked.
+      softmax_scale: defaults to ``D ** -0.5``.
+    Returns:
+      ``(o [B,S,H,D] bf16, lse [B,S,H] fp32)``.  A row with no valid index
+      gets ``o = 0`` and ``lse = sink`` (or ``-1e30`` if the sink is ``-inf``).
+    """
+    del block_h, block_n
+    assert q.is_cuda and kv.is_cuda
+    assert q.dim() == 4 and kv.dim() == 3
+    assert q.dtype in (torch.bfloat16, torch.float16), f"Q must be bf16 or fp16, got {q.dtype}"
+    assert kv.dtype == q.dtype
+    assert attn_sink.dtype == torch.float32
+    B, S, H, D = q.shape
+    B2, N_kv, D2 = kv.shape
+    assert B2 == B and D2 == D, "q and kv shape mismatch"
+    assert attn_sink.shape == (H,)
+    assert topk_idxs.shape[:2] == (B, S)
+    assert topk_idxs.dim() == 3
+    if q.dtype != torch.bfloat16:
+        raise ValueError("only bfloat16 q/kv are supported on MI355X")
+    if D not in SUPPORTED_D:
+        raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
+    if H > MAX_HEADS:
+        raise ValueError(f"H ({H}) must be <= {MAX_HEADS}")
+    if topk_idxs.dtype not in (torch.int32, torch.int64):
+        topk_idxs = topk_idxs.to(torch.int64)
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    K = topk_idxs.shape[-1]
+
+    def ok(t):
+        return t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+
+    if not ok(q):
+        q = q.contiguous()
+    if not ok(kv):
+        kv = kv.contiguous()
+    attn_sink = attn_sink.contiguous()
+    o = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=q.device)
+    L = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = L.si_sparse_attn_fwd(
+            q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
+            topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
+            B, S, H, D, N_kv, K, float(softmax_scale), o.data_ptr(), _lib.strides(o),
+            lse.data_ptr(), _lib.strides(lse), _lib.stream_ptr(q.device))
+    _lib.check(rc)
+    return o, lse
+
+
+class _SparseAttnFunc(torch.autograd.Function):
+    """Forward-only autograd wrapper (``flash_sparse/triton/__init__.py:19-44``)."""
+
+    @staticmethod
+    def forward(ctx, q, kv, attn_sink, topk_idxs, softmax_scale):
+        o, _ = sparse_attn_fwd(q, kv, attn_sink, topk_idxs, softmax_scale)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError("sparse_attn backward is not implemented on MI355X (forward-only hot path)")
+
+
+def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = None) -> torch.Tensor:
+    """Sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``)."""
+    return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale)
+
+
+__all__ = ["sparse_attn_fwd", "sparse_attn"]
