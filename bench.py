@@ -1,6 +1,7 @@
-"""Benchmark of the StreamIndex MI355X hot path (BASELINE.json metric).
+"""Benchmark of the StreamIndex MI355X hot path.
 
-Default workload = BASELINE config[1]: the V4-Flash indexer on one MI355X,
+Metric: V4-Flash indexer ms at S=64K and S=1M, MFMA utilisation, peak HBM.
+Default workload: the V4-Flash indexer on one MI355X,
 B=1, S=65,536, H_I=64, D_I=128, T=16,384, top_k=512, causal_ratio=4,
 chunk_s=2048, chunk_t=8192, seeded bf16/fp32 synthetic inputs resident in HBM.
 One "step" = one ``chunked_indexer_topk`` call (one launch of the fused
@@ -37,7 +38,9 @@ from streamindex_amd import _lib  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
-REF_H200_MS = {65536: 122.2, 1048576: 30899.6}  # BASELINE.md §1.1 (H200, not this hardware)
+# Reference timings on one H200 (other hardware; context only):
+# benchmarks/results/2026-04-27/scaling_v4_flash_indexer_final.log:10,14
+REF_H200_MS = {65536: 122.2, 1048576: 30899.6}
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -151,7 +154,24 @@ def main():
     ap.add_argument("--no-long", action="store_true", help="skip the S=1M indexer measurement")
     ap.add_argument("--no-attn", action="store_true", help="skip the sparse-attention measurement")
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
+    ap.add_argument("--only-attn", action="store_true", help="sparse-attention timing only (for profilers)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run 5 plain device copies of MIB MiB (scales HBM byte counters) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_mib": args.calibrate_copy, "launches": 5}), flush=True)
+        return
+    if args.only_attn:
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup)
+        print(json.dumps({"sparse_attn_ms": ra["ms"], "tflops": ra["flops"] / ra["ms"] / 1e9,
+                          "unique_gbps": ra["unique_bytes"] / ra["ms"] / 1e6}), flush=True)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -219,7 +239,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)-scaled, BASELINE config[1])",
+        "data": "synthetic (seeded N(0,1)-scaled bf16 q/k_idx, N(0,1) fp32 weights)",
         "config": {"workload": "v4_flash_indexer_c1", "B": 1, "S": args.seq, "T": args.seq // args.ratio,
                    "H_I": 64, "D_I": 128, "top_k": args.top_k, "causal_ratio": args.ratio,
                    "chunk_s": args.chunk_s, "chunk_t": args.chunk_t},

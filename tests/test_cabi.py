@@ -1,0 +1,159 @@
+"""CPU-only checks of the C ABI boundary (no kernel is launched).
+
+* libstreamindex.so exists, loads, and exports every entry point declared in
+  include/streamindex.h; the ctypes binding covers exactly those entries.
+* Host-side argument validation returns the documented status codes before
+  any HIP call, and the Python layer maps them to the reference's exception
+  types (AssertionError for device/shape, ValueError for unsupported dims,
+  as flash_sparse/triton/indexer_score.py:138-150 and sparse_attn_fwd.py:205-218).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from streamindex_amd import _lib
+from streamindex_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "streamindex.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(si_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("libstreamindex.so not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_expected_entries():
+    names = _declared()
+    for n in ("si_indexer_topk", "si_indexer_score", "si_sparse_attn_fwd", "si_last_error", "si_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (si_[a-z0-9_]+)\b", out))
+    declared = set(_declared())
+    assert declared <= exported, f"missing exports: {declared - exported}"
+    for n in declared:
+        assert hasattr(lib, n)
+    assert set(_lib.SIGNATURES) == declared
+
+
+def test_version_and_workspace(lib):
+    assert lib.si_abi_version() == 1
+    assert lib.si_indexer_topk_workspace_bytes(1, 1 << 20, 1 << 18, 64, 128, 512) == 0
+
+
+def _i64(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+def test_c_validation_codes_without_gpu(lib):
+    qs, ks, ws = _i64(8 * 64 * 128, 64 * 128, 128, 1), _i64(4 * 128, 128, 1), _i64(8 * 64, 64, 1)
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+    # null strides
+    rc = lib.si_indexer_topk(fake, None, fake, ks, fake, 0, ws, None, None, 1, 8, 4, 64, 128, 4, 4, fake, fake, None)
+    assert rc == _lib.SI_ERR_INVALID and b"stride" in lib.si_last_error()
+    # top_k = 0
+    rc = lib.si_indexer_topk(fake, qs, fake, ks, fake, 0, ws, None, None, 1, 8, 4, 64, 128, 0, 4, fake, fake, None)
+    assert rc == _lib.SI_ERR_INVALID and b"top_k" in lib.si_last_error()
+    # mask and ratio together
+    rc = lib.si_indexer_topk(fake, qs, fake, ks, fake, 0, ws, fake, _i64(32, 4, 1), 1, 8, 4, 64, 128, 4, 4,
+                             fake, fake, None)
+    assert rc == _lib.SI_ERR_INVALID and b"either" in lib.si_last_error()
+    # non-contiguous head dim
+    rc = lib.si_indexer_topk(fake, _i64(8 * 64 * 128, 64 * 128, 128, 2), fake, ks, fake, 0, ws, None, None,
+                             1, 8, 4, 64, 128, 4, 4, fake, fake, None)
+    assert rc == _lib.SI_ERR_INVALID
+    # unsupported shape (D=48) is reported as such
+    rc = lib.si_indexer_topk(fake, _i64(8 * 64 * 48, 64 * 48, 48, 1), fake, _i64(4 * 48, 48, 1), fake, 0, ws,
+                             None, None, 1, 8, 4, 64, 48, 4, 4, fake, fake, None)
+    assert rc == _lib.SI_ERR_UNSUPPORTED and b"D_I=48" in lib.si_last_error()
+    # top_k beyond the kernel limit
+    rc = lib.si_indexer_topk(fake, qs, fake, ks, fake, 0, ws, None, None, 1, 8, 4, 64, 128, 4096, 4, fake, fake,
+                             None)
+    assert rc == _lib.SI_ERR_UNSUPPORTED
+    # sparse attention: unsupported head dim
+    o4 = _i64(64 * 100, 64 * 100, 100, 1)
+    rc = lib.si_sparse_attn_fwd(fake, o4, fake, _i64(100 * 16, 100, 1), fake, fake, 1, _i64(32, 8, 1),
+                                1, 4, 64, 100, 16, 8, 0.1, fake, o4, fake, _i64(256, 64, 1), None)
+    assert rc == _lib.SI_ERR_INVALID or rc == _lib.SI_ERR_UNSUPPORTED
+    # empty problems succeed without touching memory
+    rc = lib.si_indexer_topk(None, qs, fake, ks, None, 0, ws, None, None, 1, 0, 4, 64, 128, 4, 4, None, None, None)
+    assert rc == _lib.SI_OK
+    # ... but a non-empty key set still needs its pointer
+    rc = lib.si_indexer_topk(None, qs, None, ks, None, 0, ws, None, None, 1, 0, 4, 64, 128, 4, 4, None, None, None)
+    assert rc == _lib.SI_ERR_INVALID
+
+
+def test_python_layer_errors_on_cpu_tensors():
+    from streamindex_amd import chunked_indexer_topk, indexer_score, sparse_attn_fwd
+
+    q = torch.zeros(1, 8, 16, 32, dtype=torch.bfloat16)
+    k = torch.zeros(1, 4, 32, dtype=torch.bfloat16)
+    w = torch.zeros(1, 8, 16)
+    with pytest.raises(AssertionError):
+        chunked_indexer_topk(q, k, w, 4, causal_ratio=4)
+    with pytest.raises(AssertionError):
+        indexer_score(q, k, w)
+    with pytest.raises(AssertionError):
+        sparse_attn_fwd(torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16), torch.zeros(1, 4, 64, dtype=torch.bfloat16),
+                        torch.zeros(16), torch.zeros(1, 2, 4, dtype=torch.int64))
+
+
+def test_error_mapping():
+    _lib.check(_lib.SI_OK)
+    if os.path.exists(LIB_PATH):
+        with pytest.raises(ValueError):
+            _lib.check(_lib.SI_ERR_INVALID)
+        with pytest.raises(ValueError):
+            _lib.check(_lib.SI_ERR_UNSUPPORTED)
+        with pytest.raises(RuntimeError):
+            _lib.check(_lib.SI_ERR_LAUNCH)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(_lib.ExtensionNotBuilt):
+        _lib.load()
+
+
+def test_reference_import_paths():
+    import flash_sparse.triton as ft
+    from flash_sparse.triton.chunked_indexer import chunked_indexer_topk
+    from flash_sparse.triton.indexer_score import indexer_score, indexer_score_topk
+    from flash_sparse.triton.sparse_attn_fwd import sparse_attn_fwd
+
+    import streamindex_amd as si
+
+    assert chunked_indexer_topk is si.chunked_indexer_topk
+    assert indexer_score is si.indexer_score and indexer_score_topk is si.indexer_score_topk
+    assert sparse_attn_fwd is si.sparse_attn_fwd and ft.sparse_attn is si.sparse_attn
+
+
+def test_synth_legal_pairs_closed_form():
+    from streamindex_amd import synth
+
+    for S in (1, 3, 4, 5, 17, 64, 1000):
+        for T in (0, 1, 3, 16, 100, 5000):
+            for r in (1, 2, 4, 7):
+                assert synth.legal_pairs(S, T, r) == sum(min(T, (s + 1) // r) for s in range(S))
+    S = 1 << 16
+    assert synth.legal_pairs(S, S // 4, 4) == S * S // 8 - S // 4
+    assert synth.indexer_flops(S, S // 4, 64, 128, 4) == 2.0 * 64 * 128 * (S * S // 8 - S // 4)

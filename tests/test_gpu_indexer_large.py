@@ -1,0 +1,78 @@
+"""Full-size indexer parity: S=65,536 (T=16,384) and S=1,048,576 (T=262,144),
+H_I=64, D_I=128, top_k=512, causal_ratio=4 — the V4-Flash shapes.
+
+The CPU oracle cannot materialise these problems, so parity is checked two ways:
+
+* sampled rows through the full oracle gate (tests/indexer_check.py);
+* size-independent properties over EVERY row, computed on the GPU with torch:
+  the valid count is exactly min(top_k, (s+1)//4), every index is causal-legal,
+  indices are distinct, scores are sorted with -1/-inf padding, and a random
+  subset of returned scores recomputes (torch fp32 matmul) to 1e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from streamindex_amd import chunked_indexer_topk, synth
+from tests.indexer_check import check_indexer
+
+pytestmark = pytest.mark.gpu
+
+
+def _properties(q, k, w, idx, sc, top_k, ratio, nprobe=4096, seed=0):
+    B, S, H, D = q.shape
+    T = k.shape[1]
+    dev = idx.device
+    s = torch.arange(S, device=dev)
+    lim = torch.clamp((s + 1) // ratio, max=T)
+    nvalid = (idx[0] >= 0).sum(-1)
+    assert torch.equal(nvalid, torch.clamp(lim, max=top_k)), "valid count != min(top_k, legal keys)"
+    slot = torch.arange(top_k, device=dev)
+    valid = slot[None, :] < nvalid[:, None]
+    assert bool((idx[0][~valid] == -1).all()) and bool(torch.isneginf(sc[0][~valid]).all())
+    assert bool((idx[0][valid] >= 0).all())
+    assert bool((idx[0] < lim[:, None]).all()), "returned a future (illegal) key"
+    d = sc[0][:, :-1] - sc[0][:, 1:]
+    both = valid[:, 1:]
+    assert bool((d[both] >= 0).all()), "scores not sorted"
+    srt = torch.sort(idx[0], dim=-1).values
+    dup = (srt[:, 1:] == srt[:, :-1]) & (srt[:, 1:] >= 0)
+    assert not bool(dup.any()), "duplicate index in a row"
+    # recompute a random subset of returned scores in fp32 on the GPU
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    rows = torch.randint(ratio * 2, S, (nprobe,), generator=g).to(dev)
+    cols = (torch.rand(nprobe, generator=g).to(dev) * torch.clamp(nvalid[rows], min=1)).long()
+    ti = idx[0, rows, cols]
+    qk = torch.einsum("nhd,nd->nh", q[0, rows].float(), k[0, ti].float())
+    ref = (qk.relu() * w[0, rows].float()).sum(-1)
+    got = sc[0, rows, cols]
+    scale = ref.abs().mean()
+    err = (got - ref).abs()
+    assert bool((err <= 1e-4 * (ref.abs() + scale)).all()), f"recomputed score error {err.max().item():.3e}"
+
+
+def test_c1_s64k_full_size():
+    S, ratio, top_k = 65536, 4, 512
+    q, k, w = synth.indexer_inputs(1, S, 64, 128, ratio=ratio, seed=2026, device="cuda")
+    idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)
+    torch.cuda.synchronize()
+    _properties(q, k, w, idx, sc, top_k, ratio)
+    rows = np.sort(np.random.default_rng(1).choice(S, 768, replace=False))
+    rows = np.concatenate([[0, 1, 2, 3, 2047, 2048, S - 1], rows])
+    st = check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, rows=np.unique(rows), label="S=64K")
+    assert st[0]["recall_mean"] >= 0.999
+
+
+def test_c4_s1m_indexer_stage():
+    S, ratio, top_k = 1 << 20, 4, 512
+    q, k, w = synth.indexer_inputs(1, S, 64, 128, ratio=ratio, seed=2026, device="cuda")
+    idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio)
+    torch.cuda.synchronize()
+    _properties(q, k, w, idx, sc, top_k, ratio)
+    rows = np.sort(np.random.default_rng(2).choice(S, 96, replace=False))
+    rows = np.unique(np.concatenate([[3, 4095, S - 1], rows]))
+    st = check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, rows=rows, label="S=1M")
+    assert st[0]["recall_mean"] >= 0.999

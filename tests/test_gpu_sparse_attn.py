@@ -116,7 +116,7 @@ def test_head_counts(cuda_device, H):
 
 
 def test_v4_shape_with_indexer_indices(cuda_device):
-    # BASELINE config[3] layout at small S: indices from the fused indexer.
+    # V4 CSA layout (64 heads, D=576, ratio 4) at small S: indices from the fused indexer.
     from streamindex_amd import chunked_indexer_topk
 
     S, T = 512, 128
