@@ -1,0 +1,39 @@
+// Lightning-indexer kernel interface shared by the C-ABI entry (indexer.hip)
+// and the per-shape instantiation units (indexer_inst_d*.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace si {
+
+struct IndexerArgs {
+  const uint16_t* q;  // [B,S,H,D] bf16, d contiguous
+  int64_t qsb, qss, qsh;
+  const uint16_t* k;  // [B,T,D] bf16, d contiguous
+  int64_t ksb, kst;
+  const void* w;      // [B,S,H] fp32 or bf16
+  int64_t wsb, wss, wsh;
+  int w_bf16;
+  const uint8_t* mask;  // optional [B,S,T] bool (nonzero = legal)
+  int64_t msb, mss, mst;
+  int B, S, T, H;
+  int top_k;
+  int ratio;  // > 0: legal iff t < (s+1)/ratio; 0: no causal bound
+  int64_t* out_idx;     // [B,S,top_k] contiguous
+  float* out_scores;    // [B,S,top_k] contiguous
+  float* scores;        // score kernel: [B,S,T]
+  int64_t ssb, sss, sst;
+};
+
+// Selection-buffer capacities the top-k kernel is instantiated for.
+// Capacity C serves top_k <= C / 2 (and at least C - 64 >= top_k).
+constexpr int kTopkCaps[] = {256, 512, 1024, 2048, 4096};
+
+template <int HB, int D, int C>
+int launch_topk(const IndexerArgs& a, hipStream_t st);
+
+template <int HB, int D>
+int launch_score(const IndexerArgs& a, hipStream_t st);
+
+}  // namespace si

@@ -1,0 +1,7 @@
+// Instantiates the lightning-indexer kernels for head dim D_I = 128.
+#include "indexer_kernels.h"
+
+namespace si {
+SI_INSTANTIATE_INDEXER(1, 128)
+SI_INSTANTIATE_INDEXER(2, 128)
+}  // namespace si
