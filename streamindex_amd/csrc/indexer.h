@@ -26,9 +26,9 @@ struct IndexerArgs {
   int64_t ssb, sss, sst;
 };
 
-// Selection-buffer capacities the top-k kernel is instantiated for.
-// Capacity C serves top_k <= C / 2 (and at least C - 64 >= top_k).
-constexpr int kTopkCaps[] = {256, 512, 1024, 2048, 4096};
+// Selection-buffer capacities the top-k kernel is instantiated for: 256,
+// 512, 1024, 2048 and 4096 keys per query row (capacity C serves
+// top_k <= C - 192).
 
 template <int HB, int D, int C>
 int launch_topk(const IndexerArgs& a, hipStream_t st);

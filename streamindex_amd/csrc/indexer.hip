@@ -9,10 +9,12 @@ namespace si {
 
 template <int HB, int D>
 static int dispatch_kcap(const IndexerArgs& a, hipStream_t st) {
-  if (a.top_k <= 128) return launch_topk<HB, D, 256>(a, st);
-  if (a.top_k <= 256) return launch_topk<HB, D, 512>(a, st);
-  if (a.top_k <= 512) return launch_topk<HB, D, 1024>(a, st);
-  if (a.top_k <= 1024) return launch_topk<HB, D, 2048>(a, st);
+  // A compaction keeps between top_k and C - 192 keys; the capacity is
+  // chosen so that this window leaves room for several 64-key offers.
+  if (a.top_k <= 32) return launch_topk<HB, D, 256>(a, st);
+  if (a.top_k <= 192) return launch_topk<HB, D, 512>(a, st);
+  if (a.top_k <= 640) return launch_topk<HB, D, 1024>(a, st);
+  if (a.top_k <= 1536) return launch_topk<HB, D, 2048>(a, st);
   if (a.top_k <= 2048) return launch_topk<HB, D, 4096>(a, st);
   return set_error(SI_ERR_UNSUPPORTED, "top_k > 2048 is not supported");
 }

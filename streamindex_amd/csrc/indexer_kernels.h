@@ -10,20 +10,26 @@
 //
 // Design (one query row per wavefront, NW rows per workgroup):
 //   * The row's Q block [H, D] lives in VGPRs as MFMA A-fragments (heads on
-//     the M axis), loaded once.  K tiles of TILE_N keys are streamed through
-//     a double-buffered, XOR-swizzled LDS ring shared by the workgroup; the
-//     global loads of tile i+1 are in flight while tile i is consumed.
-//   * Per 32-key block, v_mfma_f32_32x32x16_bf16 produces [32 heads x 32 keys]
-//     per M-block; lane l holds key l%32 for 16 heads, so ReLU (v_med3) and
-//     the fp32 weighted head sum are in-lane, finished by one xor-32 exchange.
-//     B-fragments of block nb+1 are read from LDS while block nb's MFMAs run.
+//     the M axis), loaded once.  K tiles are copied HBM/L2 -> LDS by
+//     global_load_lds into a double-buffered, XOR-swizzled ring shared by the
+//     workgroup; tile i+1 is in flight while tile i is consumed.
+//   * v_mfma_f32_32x32x16_bf16 produces [32 heads x 32 keys] per M-block
+//     ("group"); lane l holds key l%32 for 16 heads, so ReLU (v_med3) and the
+//     fp32 weighted head sum are in-lane.
+//   * Top-k kernel: the groups of a tile are software-pipelined.  Group g's
+//     MFMAs accumulate into one of two accumulator sets while the epilogue of
+//     group g-1 (ReLU + weighted sum) reads the other, and the next 32-key
+//     block's B-fragments are read from LDS behind the MFMAs that consume the
+//     current ones.  The two half-wave partial sums of a 64-key tile are
+//     combined with one v_permlane32_swap and the tile's 64 keys are offered
+//     to the wave's selection buffer (wave_select.h) in one branch-free
+//     append, overlapped with the next tile's first MFMAs.
 //   * The causal bound t < (s+1)//ratio is evaluated per lane in registers;
-//     tiles past the workgroup's last legal key are never loaded or computed.
-//   * The top-k kernel never writes scores: each lane offers its key to the
-//     wave's selection buffer (wave_select.h); the score kernel stores the
-//     fp32 row instead.
+//     32-key blocks past a row's bound are skipped and tiles past the
+//     workgroup's last legal key are never loaded.
 //   * Workgroups are issued heaviest-first (the last query block first) so the
-//     triangular causal workload drains evenly over the 256 CUs.
+//     triangular causal workload drains evenly; two workgroups share a CU so
+//     one's barriers, compactions and final sort overlap the other's MFMAs.
 #pragma once
 
 #include "indexer.h"
@@ -31,11 +37,13 @@
 #include "si_status.h"
 #include "wave_select.h"
 
+#include <type_traits>
+
 namespace si {
 
 // Byte offset of 16-byte chunk c of key row r inside a swizzled K tile.
 // The XOR spreads the 16 rows read by one ds_read_b128 quarter-wave over
-// distinct bank groups.
+// distinct bank groups.  The pattern repeats every 16 rows.
 template <int D>
 __device__ __forceinline__ int kt_off(int r, int c) {
   constexpr int CPR = D / 8;                          // 16-byte chunks per row
@@ -123,6 +131,18 @@ struct QueryFrags {
       kb[ks] = *reinterpret_cast<const bf16x8*>(tile + kt_off<D>(row, ks * 2 + (lane >> 5)));
   }
 
+  // Sum over this lane's 16 heads of M-block mb: sum_v w_v * relu(acc_v).
+  __device__ __forceinline__ float epilogue(const f32x16& acc, int mb) const {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      // relu as a single v_med3_f32 (clamp to [0, FLT_MAX])
+      s0 = __builtin_fmaf(wf[mb][v], __builtin_amdgcn_fmed3f(acc[v], 0.f, __FLT_MAX__), s0);
+      s1 = __builtin_fmaf(wf[mb][v + 1], __builtin_amdgcn_fmed3f(acc[v + 1], 0.f, __FLT_MAX__), s1);
+    }
+    return s0 + s1;
+  }
+
   // Score of key (block base + lane%32) for this row; identical in lanes l and l+32.
   __device__ __forceinline__ float score(const bf16x8 (&kb)[KS], int lane) const {
     f32x16 acc[HB];
@@ -137,13 +157,7 @@ struct QueryFrags {
     }
     float sum = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < HB; ++mb) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        // relu as a single v_med3_f32 (clamp to [0, FLT_MAX])
-        sum = __builtin_fmaf(wf[mb][v], __builtin_amdgcn_fmed3f(acc[mb][v], 0.f, __FLT_MAX__), sum);
-      }
-    }
+    for (int mb = 0; mb < HB; ++mb) sum += epilogue(acc[mb], mb);
     return sum + shfl_xor_f32(sum, lane, 32);
   }
 
@@ -165,6 +179,19 @@ struct QueryFrags {
   }
 };
 
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time loop).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_impl(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_impl<I + 1, N>(f);
+  }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F& f) {
+  static_for_impl<0, N>(f);
+}
+
 __device__ __forceinline__ int legal_limit(const IndexerArgs& a, int s) {
   if (a.ratio > 0) {
     const int l = (s + 1) / a.ratio;
@@ -173,22 +200,40 @@ __device__ __forceinline__ int legal_limit(const IndexerArgs& a, int s) {
   return a.T;
 }
 
+// Launch shape of the top-k kernel per selection capacity C: four rows per
+// workgroup and 64-key tiles.  Up to C = 1024 a workgroup needs at most
+// 2*16 KiB (ring) + 4*8 KiB (selection) = 64 KiB of LDS and 256 VGPRs per
+// wave, so two workgroups share a CU; wider capacities run one per CU.
+template <int C>
+struct TopkShape {
+  static constexpr int NW = 4;
+  static constexpr int TILE_N = 64;
+  static constexpr int WAVES_PER_EU = C <= 1024 ? 2 : 1;
+};
+
 // ---------------------------------------------------------------------------
 // Fused score + streaming exact top-k.
 // ---------------------------------------------------------------------------
-template <int HB, int D, int C, int NW, int TILE_N>
-__global__ __launch_bounds__(NW * 64, 1) void indexer_topk_kernel(IndexerArgs a) {
+template <int HB, int D, int C, bool MASKED>
+__global__ __launch_bounds__(TopkShape<C>::NW * 64)
+__attribute__((amdgpu_waves_per_eu(TopkShape<C>::WAVES_PER_EU, TopkShape<C>::WAVES_PER_EU)))
+void indexer_topk_kernel(IndexerArgs a) {
+  constexpr int NW = TopkShape<C>::NW;
   constexpr int NT = NW * 64;
-  constexpr int NB = TILE_N / 32;
+  constexpr int TILE_N = TopkShape<C>::TILE_N;
+  constexpr int NB = TILE_N / 32;  // 32-key blocks per tile
+  static_assert(NB == 2, "one 64-key offer per tile");
+  constexpr int KS = D / 16;       // MFMA k-steps per 32-key block
+  constexpr int G = NB * HB;       // MFMA groups per tile (even)
   constexpr int TILE_BYTES = TILE_N * D * 2;
-  // One LDS arena: the DMA-filled K ring first (offsets below 64 KiB, the
-  // range global_load_lds destinations are kept in), then the per-wave
-  // selection buffers.
+  constexpr int BLK_BYTES = 32 * D * 2;
+  // The DMA-filled K ring sits first (global_load_lds destinations stay
+  // below 64 KiB), then the per-wave selection buffers.
   __shared__ __attribute__((aligned(16))) char lds[2 * TILE_BYTES + NW * C * 8];
   uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + 2 * TILE_BYTES);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nqb = (a.S + NW - 1) / NW;
   const int b = blockIdx.x % a.B;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x / a.B);  // heaviest first
@@ -202,43 +247,137 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_topk_kernel(IndexerArgs a)
   QueryFrags<HB, D> qfr;
   if (active) qfr.load(a, b, s, lane);
 
+  // Per-lane B-fragment offsets of block 0 (block 1 is BLK_BYTES further on:
+  // the swizzle repeats every 16 rows).
+  int boff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) boff[ks] = kt_off<D>(lane & 31, ks * 2 + (lane >> 5));
+
+  // Which 32-key block of a tile this lane offers after the half-wave swap.
+  const int oblk = static_cast<int>(permlane32_swap(0u, 1u).x);
+  const int okey = oblk * 32 + (lane & 31);
+
   WaveSelect<C> sel;
   sel.init(sel_base + wave * C, a.top_k);
 
   const uint16_t* kb = a.k + b * a.ksb;
   const uint8_t* mrow =
-      a.mask ? a.mask + b * a.msb + static_cast<int64_t>(active ? s : 0) * a.mss : nullptr;
+      MASKED ? a.mask + b * a.msb + static_cast<int64_t>(active ? s : 0) * a.mss : nullptr;
 
   const KTileLoader<D, TILE_N, NT> ld;
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
   if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
+
+  // Pipeline state carried across tiles.  Each of the G groups of a tile has
+  // its own accumulator; the epilogue runs LAG = HB groups behind the MFMAs,
+  // so it never waits on the chain that was just issued.  At a tile boundary
+  // the previous tile's block-1 groups (acc[HB..G-1]) are still pending,
+  // together with the half-wave partial sum of its block 0.
+  constexpr int LAG = HB;
+  f32x16 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x16{};
+  float prev_p0 = 0.f;
+  int prev_tbase = 0;
+  bool pend = false;
+  bool prev_mask = true, cur_mask = true;
+
+  auto offer_tile = [&](float p0, float p1, int tbase, bool valid, bool mok) {
+    const SwapPair r = permlane32_swap(__float_as_uint(p0), __float_as_uint(p1));
+    const float sum = __uint_as_float(r.x) + __uint_as_float(r.y);
+    const int t = tbase + okey;
+    const bool legal = valid && t < my_lim && mok;
+    const uint64_t key = make_key(sum, static_cast<uint32_t>(t));
+    sel.offer64(legal && key_hi(key) > sel.tau, key, lane);
+  };
+  // Epilogues of the pending block-1 groups of the previous tile, then its offer.
+  auto drain = [&]() {
+    float p1 = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < HB; ++mb) p1 += qfr.epilogue(acc[HB + mb], mb);
+    offer_tile(prev_p0, p1, prev_tbase, true, prev_mask);
+  };
+
   tile_barrier();
 
   for (int it = 0; it < ntiles; ++it) {
-    const bool more = it + 1 < ntiles;
-    if (more) ld.issue(kb, a.kst, (it + 1) * TILE_N, a.T, lds + ((it + 1) & 1) * TILE_BYTES);
+    if (it + 1 < ntiles) ld.issue(kb, a.kst, (it + 1) * TILE_N, a.T, lds + ((it + 1) & 1) * TILE_BYTES);
     const char* tile = lds + (it & 1) * TILE_BYTES;
     const int tbase = it * TILE_N;
+    if constexpr (MASKED) {
+      const int t = tbase + okey;
+      cur_mask = t < my_lim ? mrow[static_cast<int64_t>(t) * a.mst] != 0 : false;
+    }
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
-    float sc[NB];
+
     if (nblk == NB) {
-      qfr.template tile_scores<NB, true>(tile, NB, lane, sc);
-    } else if (nblk > 0) {
-      qfr.template tile_scores<NB, false>(tile, nblk, lane, sc);
-    }
+      // ---- full tile: software-pipelined groups ---------------------------
+      bf16x8 kf[KS];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (nb < nblk) {
-        const int t = tbase + nb * 32 + (lane & 31);
-        bool legal = (lane < 32) && (t < my_lim);
-        if (mrow != nullptr && legal) legal = mrow[static_cast<int64_t>(t) * a.mst] != 0;
-        const uint64_t key = make_key(sc[nb], static_cast<uint32_t>(t));
-        sel.offer(legal && key_hi(key) > sel.tau, key, lane);
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks]);
+      __builtin_amdgcn_sched_barrier(0);  // all block-0 reads in flight before the first MFMA
+      float p0 = 0.f, p1 = 0.f;
+      auto phase = [&](auto PHC) {
+        constexpr int ph = decltype(PHC)::value;
+        constexpr int mb = ph % HB;
+        constexpr bool last_use = (ph == HB - 1);     // block-0 fragments retire in this group
+        constexpr int eg = (ph + G - LAG) % G;        // group whose epilogue runs now
+        constexpr int emb = eg % HB;
+        const float e = qfr.epilogue(acc[eg], emb);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          acc[ph] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qfr.qf[mb][ks], kf[ks], ks == 0 ? f32x16{} : acc[ph],
+                                                            0, 0, 0);
+          if constexpr (last_use) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks] + BLK_BYTES);
+        }
+        if constexpr (ph < LAG) {
+          p1 += e;  // previous tile, block 1
+          if constexpr (ph == LAG - 1) offer_tile(prev_p0, p1, prev_tbase, pend, prev_mask);
+        } else {
+          p0 += e;  // this tile, block 0
+        }
+        // Interleave: one MFMA, then a share of the epilogue / offer VALU work.
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if constexpr (last_use) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, ph == LAG - 1 ? 7 : 4, 0);
+        }
+      };
+      static_for<G>(phase);
+      (void)p1;
+      prev_p0 = p0;
+      prev_tbase = tbase;
+      prev_mask = cur_mask;
+      pend = true;
+    } else {
+      // ---- partial tile (the row's causal edge): drain, then one block ------
+      if (pend) {
+        drain();
+        pend = false;
+      }
+      if (nblk == 1) {
+        bf16x8 kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks]);
+        float p0 = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < HB; ++mb) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qfr.qf[mb][ks], kf[ks], ks == 0 ? f32x16{} : acc[0],
+                                                             0, 0, 0);
+          p0 += qfr.epilogue(acc[0], mb);
+        }
+        offer_tile(p0, 0.f, tbase, true, cur_mask);
       }
     }
+    if (sel.needs_compaction()) sel.compact(lane);
     tile_barrier();
   }
+
+  if (pend) drain();
 
   if (active) {
     const int64_t row = static_cast<int64_t>(b) * a.S + s;
@@ -300,23 +439,19 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-template <int C>
-struct TopkLaunchShape {
-  // (waves per workgroup, keys per LDS tile) so that NW*C*8 + 2*TILE_N*D*2 <= 160 KiB
-  // and the K ring (2*TILE_N*D*2 <= 64 KiB) stays where the tile DMA can address it
-  static constexpr int NW = C <= 1024 ? 8 : 4;
-  static constexpr int TILE_N = C <= 2048 ? 128 : 64;
-};
-
 template <int HB, int D, int C>
 int launch_topk(const IndexerArgs& a, hipStream_t st) {
-  constexpr int NW = TopkLaunchShape<C>::NW;
-  constexpr int TILE_N = TopkLaunchShape<C>::TILE_N;
+  constexpr int NW = TopkShape<C>::NW;
   const int nqb = (a.S + NW - 1) / NW;
   const int64_t nblk = static_cast<int64_t>(nqb) * a.B;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((indexer_topk_kernel<HB, D, C, NW, TILE_N>), dim3(static_cast<unsigned>(nblk)),
-                     dim3(NW * 64), 0, st, a);
+  if (a.mask) {
+    hipLaunchKernelGGL((indexer_topk_kernel<HB, D, C, true>), dim3(static_cast<unsigned>(nblk)), dim3(NW * 64),
+                       0, st, a);
+  } else {
+    hipLaunchKernelGGL((indexer_topk_kernel<HB, D, C, false>), dim3(static_cast<unsigned>(nblk)), dim3(NW * 64),
+                       0, st, a);
+  }
   return check_launch("indexer_topk_kernel");
 }
 

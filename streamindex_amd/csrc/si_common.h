@@ -61,6 +61,35 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int mask)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
+// Half-wave exchange (v_permlane32_swap): returns {a', b'} where a' and b'
+// together hold a's and b's 32-lane halves regrouped so that, in every lane,
+// a' and b' come from the same source register (a or b) and from the two
+// different halves.  Which of a/b a lane ends up with is reported by
+// swapping an id vector the same way.
+struct SwapPair {
+  uint32_t x, y;
+};
+__device__ __forceinline__ SwapPair permlane32_swap(uint32_t a, uint32_t b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  return SwapPair{static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1])};
+}
+
+// Wave-wide maximum of an unsigned value, returned uniformly.  Within each
+// 16-lane row: xor-1 and xor-2 (quad_perm), then the half-row and row
+// mirrors; across rows: v_permlane16_swap and v_permlane32_swap.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0xB1, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x4E, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x141, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x140, 0xf, 0xf, false)));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = mx(static_cast<uint32_t>(r16[0]), static_cast<uint32_t>(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  x = mx(static_cast<uint32_t>(r32[0]), static_cast<uint32_t>(r32[1]));
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+}
+
 // Number of set bits of `m` in lanes strictly below this lane.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),

@@ -3,20 +3,24 @@
 // One wave owns the selection state of one query row:
 //   * `buf`   : an unsorted LDS buffer of capacity C holding every key seen so
 //               far that is >= the floor key P (and nothing below it);
-//   * `floor` : P, raised only when the buffer fills; count(buf) >= top_k
-//               always holds once P > 0, so no key below P can be in the top-k;
+//   * `floor` : P, raised only when the buffer nears capacity; once P > 0,
+//               count(buf) >= top_k always holds, so no key below P can be in
+//               the top-k;
 //   * `tau`   : the high word (ordered score) of P.
-// A new key arrives with an index larger than every index already seen, so
-// if its ordered score equals tau it ranks below every buffered key >= P and
-// the arrival filter is the strict test `ord(score) > tau` (exact).
+// Keys arrive in increasing index order, so an arriving key whose ordered
+// score equals tau ranks below every buffered key with that score (ties rank
+// the smaller index first) and the arrival filter is the strict test
+// `ord(score) > tau` (exact).
 //
-// When the buffer cannot take another 32 keys it is compacted: a new floor P'
-// is chosen so that top_k <= count(keys >= P') <= C - 64, using 64 evenly
-// spaced samples (bitonic-sorted across the wave) and, if needed, bisection
-// over the 64-bit key space.  Keys are distinct, so the count drops by at most
-// one per key value and bisection always lands in the window.  Counting is a
-// ballot per 64-key row, so a compaction costs ~C/64 compares, not a sort.
-// The exact sorted top-k is produced once, at the end of the row.
+// Offers append up to 64 keys at a time without branches.  When the buffer
+// holds more than C - 128 keys it is compacted: the keys are pulled into
+// registers (C/64 per lane), a new floor P' with
+// top_k <= count(keys >= P') <= C - 192 is found by safeguarded interpolation
+// over the ordered-score word (each probe is one ballot per 64 keys), with a
+// bisection over the full 64-bit key when many keys share one score, and the
+// survivors are written back densely.  Keys are distinct, so a count changes
+// by at most one per key value and the 64-bit bisection always lands in the
+// window.  The exact sorted top-k is produced once, at the end of the row.
 #pragma once
 
 #include "si_common.h"
@@ -77,16 +81,10 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&v)[E], int lane) {
   bitonic_levels<E, kWave * E, 2>(v, lane);
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 template <int C>
 struct WaveSelect {
   static constexpr int E = C / kWave;   // 64-key rows in the buffer
-  static constexpr int CMAX = C - 64;   // most keys kept by a compaction
+  static constexpr int CMAX = C - 192;  // most keys a compaction keeps
   static_assert(E >= 4 && (E & (E - 1)) == 0, "capacity must be 64 * 2^n, n >= 2");
 
   uint64_t* buf;        // this wave's private LDS buffer, key at position p = buf[p]
@@ -103,83 +101,115 @@ struct WaveSelect {
     top_k = k;
   }
 
-  // Offers this lane's key if `pass`; appends in lane order.
-  __device__ __forceinline__ void offer(bool pass, uint64_t key, int lane) {
+  // Appends the keys of the lanes with `pass` set, in lane order, at
+  // positions n, n+1, ...  The other lanes store to positions past the new
+  // end, which are never read, so the append has no branch.  Needs n <= C-64.
+  __device__ __forceinline__ void offer64(bool pass, uint64_t key, int lane) {
     const uint64_t bal = ballot64(pass);
-    if (bal == 0) return;
-    if (pass) buf[n + lanes_below(bal)] = key;
-    n += __builtin_popcountll(bal);
-    if (n > C - 32) compact(lane);
+    const int below = lanes_below(bal);
+    const int tot = __builtin_popcountll(bal);
+    const int pos = pass ? n + below : n + tot + (lane - below);
+    buf[pos] = key;
+    n = __builtin_amdgcn_readfirstlane(n + tot);
   }
 
-  // Number of buffered keys >= p (one ballot per 64-key row).
-  __device__ __forceinline__ int count_ge(uint64_t p, int lane) const {
+  // Compacting whenever more than C - 128 keys are held leaves room for two
+  // 64-key offers before the next check.
+  __device__ __forceinline__ bool needs_compaction() const { return n > C - 2 * kWave; }
+
+  __device__ __forceinline__ static int count_hi_ge(const uint64_t (&v)[E], uint32_t h) {
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-      const int pos = j * kWave + lane;
-      if (j * kWave < n) {
-        const uint64_t key = pos < n ? buf[pos] : 0ull;
-        c += __builtin_popcountll(ballot64(pos < n && key >= p));
-      }
-    }
+    for (int j = 0; j < E; ++j) c += __builtin_popcountll(ballot64(key_hi(v[j]) >= h));
+    return c;
+  }
+
+  __device__ __forceinline__ static int count_ge(const uint64_t (&v)[E], uint64_t p) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) c += __builtin_popcountll(ballot64(v[j] >= p));
     return c;
   }
 
   __device__ __forceinline__ void compact(int lane) {
     wave_lds_sync();
-    // 64 keys at evenly spaced buffer positions, sorted descending across lanes.
-    uint64_t smp[1];
-    smp[0] = buf[(lane * n) >> 6];
-    wave_sort_desc<1>(smp, lane);
+    uint64_t v[E];
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const int pos = j * kWave + lane;
+      v[j] = pos < n ? buf[pos] : 0ull;  // empty slots hold key 0: never counted (every probe is >= 1)
+      mx = key_hi(v[j]) > mx ? key_hi(v[j]) : mx;
+    }
+    mx = wave_max_u32(mx);
     const int kk = top_k;
-    const int target = kk + (CMAX - kk) / 3;
-    int il = -1, ih = 64;  // count(sample[il]) < kk, count(sample[ih]) > CMAX
-    int i = (target * 64) / n;
-    i = i < 0 ? 0 : (i > 63 ? 63 : i);
-    uint64_t p = 0;
+    const int target = kk + (CMAX - kk) / 4;
+
+    // Invariant: count(hi >= lo) = c_lo > CMAX and count(hi >= hi_) = c_hi < kk.
+    uint64_t lo = tau, hi_ = static_cast<uint64_t>(mx) + 1;
+    int c_lo = n, c_hi = 0;
+    uint64_t P = 0;
     int c = 0;
     bool found = false;
-    for (int it = 0; it < 7 && !found; ++it) {
-      p = readlane_u64(smp[0], i);
-      c = count_ge(p, lane);
-      if (c >= kk && c <= CMAX) {
-        found = true;
+    for (int it = 0; it < 48 && hi_ - lo > 1; ++it) {
+      const uint64_t span = hi_ - lo;
+      uint64_t step;
+      if (it & 1) {
+        step = span >> 1;
       } else {
-        if (c < kk) il = i; else ih = i;
-        if (ih - il <= 1) break;
-        i = (il + ih) >> 1;
+        const float f = static_cast<float>(c_lo - target) / static_cast<float>(c_lo - c_hi);
+        step = static_cast<uint64_t>(static_cast<float>(span) * f);
+      }
+      step = step < 1 ? 1 : (step > span - 1 ? span - 1 : step);
+      const uint32_t mid = static_cast<uint32_t>(lo + step);
+      c = count_hi_ge(v, mid);
+      if (c >= kk && c <= CMAX) {
+        P = static_cast<uint64_t>(mid) << 32;
+        found = true;
+        break;
+      }
+      if (c > CMAX) {
+        lo = mid;
+        c_lo = c;
+      } else {
+        hi_ = mid;
+        c_hi = c;
       }
     }
     if (!found) {
-      // Bisection over the key space between a floor with too many keys and a
-      // ceiling with too few; terminates because keys are distinct.
-      uint64_t lo = ih < 64 ? readlane_u64(smp[0], ih) : floor_key;
-      uint64_t hi = il >= 0 ? readlane_u64(smp[0], il) : ~0ull;
-      for (int it = 0; it < 66; ++it) {
-        p = lo + ((hi - lo) >> 1);
-        c = count_ge(p, lane);
-        if (c >= kk && c <= CMAX) break;
-        if (c < kk) hi = p; else lo = p;
+      // Many keys share the ordered score `lo`: bisect over the full key.
+      uint64_t plo = lo << 32;
+      uint64_t phi = hi_ >= (1ull << 32) ? ~0ull : (hi_ << 32);
+      for (int it = 0; it < 64 && phi - plo > 1; ++it) {
+        const uint64_t mid = plo + ((phi - plo) >> 1);
+        c = count_ge(v, mid);
+        if (c >= kk && c <= CMAX) {
+          P = mid;
+          found = true;
+          break;
+        }
+        if (c > CMAX) plo = mid; else phi = mid;
+      }
+      if (!found) {  // unreachable for distinct keys; keep the capacity bound
+        P = phi;
+        c = count_ge(v, P);
       }
     }
-    // In-place compaction: the write position never passes the read position.
+    // Dense write-back: survivors to [0, c), the rest past c (never read).
+    // Every key is already in registers, so the in-place writes are safe.
     int base = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      if (j * kWave < n) {
-        const int pos = j * kWave + lane;
-        const uint64_t key = pos < n ? buf[pos] : 0ull;
-        const bool keep = pos < n && key >= p;
-        const uint64_t bal = ballot64(keep);
-        wave_lds_sync();
-        if (keep) buf[base + lanes_below(bal)] = key;
-        base += __builtin_popcountll(bal);
-      }
+      const bool keep = v[j] >= P;
+      const uint64_t bal = ballot64(keep);
+      const int below = lanes_below(bal);
+      const int pos = keep ? base + below : c + (j * kWave + lane - base - below);
+      buf[pos] = v[j];
+      base += __builtin_popcountll(bal);
     }
-    n = base;
-    floor_key = p;
-    tau = key_hi(p);
+    n = __builtin_amdgcn_readfirstlane(c);
+    floor_key = P;
+    tau = __builtin_amdgcn_readfirstlane(key_hi(P));
     wave_lds_sync();
   }
 
@@ -198,8 +228,7 @@ struct WaveSelect {
     } else {
       // Wider buffers are sorted as two halves of 32 keys per lane: the first
       // half is parked in LDS in rank order, then one half-cleaner + bitonic
-      // merge yields the top C/2 >= top_k.  (A single 64-key-per-lane
-      // register sort is avoided: it does not fit this kernel's registers.)
+      // merge yields the top C/2 >= top_k.
       constexpr int HE = E / 2;
       constexpr int HALF = C / 2;
       uint64_t v[HE];
@@ -229,17 +258,19 @@ struct WaveSelect {
     }
   }
 
+  // Keys of rank lane*EE+j are staged through LDS in rank order so that the
+  // global stores are contiguous across the wave.
   template <int EE>
   __device__ __forceinline__ void write_out(const uint64_t (&v)[EE], int64_t* out_idx, float* out_score,
                                             int lane) const {
+    wave_lds_sync();
 #pragma unroll
-    for (int j = 0; j < EE; ++j) {
-      const int e = lane * EE + j;
-      if (e < top_k) {
-        const uint64_t k = v[j];
-        out_idx[e] = k ? static_cast<int64_t>(key_idx(k)) : int64_t(-1);
-        out_score[e] = k ? ord_to_f32(key_hi(k)) : -__builtin_inff();
-      }
+    for (int j = 0; j < EE; ++j) buf[lane * EE + j] = v[j];
+    wave_lds_sync();
+    for (int e = lane; e < top_k; e += kWave) {
+      const uint64_t k = buf[e];
+      out_idx[e] = k ? static_cast<int64_t>(key_idx(k)) : int64_t(-1);
+      out_score[e] = k ? ord_to_f32(key_hi(k)) : -__builtin_inff();
     }
   }
 };
