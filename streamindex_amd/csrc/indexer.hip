@@ -50,6 +50,8 @@ static int fill_common(IndexerArgs& a, const void* q, const int64_t* qs, const v
   if (qs[3] != 1 || ks[2] != 1) return set_error(SI_ERR_INVALID, "q and k_idx need a contiguous last dimension");
   if ((qs[2] % 8) || (qs[1] % 8) || (qs[0] % 8) || (ks[1] % 8) || (ks[0] % 8))
     return set_error(SI_ERR_INVALID, "q/k_idx strides must be multiples of 8 elements (16-byte rows)");
+  if (ks[1] < 0 || ks[1] >= (int64_t(1) << 23))  // tile loads address 128 rows with 32-bit byte offsets
+    return set_error(SI_ERR_UNSUPPORTED, "k_idx row stride must be below 2^23 elements");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15)  // null is aligned
     return set_error(SI_ERR_INVALID, "q/k_idx must be 16-byte aligned");
   if (w_dtype != 0 && w_dtype != 1) return set_error(SI_ERR_INVALID, "weights dtype must be fp32 (0) or bf16 (1)");

@@ -57,28 +57,59 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Copies one K tile straight from HBM/L2 into the swizzled LDS layout with
 // global_load_lds_dwordx4 (no staging registers).  One wave instruction
 // fills 64 consecutive 16-byte LDS slots (slot = base + lane); each lane
-// fetches the global chunk that belongs in its slot under the swizzle.
-// Rows past T re-read row T-1; those keys are never legal.
+// fetches the global chunk that belongs in its slot under the swizzle.  The
+// lane's byte offsets from the tile's first key row are computed once, so a
+// tile inside [0, T) costs one scalar base per tile; a tile that crosses T
+// re-reads row T-1 for its missing rows (those keys are never legal).
+// Needs TILE_N * k_row_stride * 2 < 2^31 (checked on the host).
 template <int D, int TILE_N, int NTHREADS>
 struct KTileLoader {
   static constexpr int CPR = D / 8;
   static constexpr int CHUNKS = TILE_N * CPR;
   static constexpr int LPT = CHUNKS / NTHREADS;
   static_assert(CHUNKS % NTHREADS == 0, "tile must split evenly over the workgroup");
+  uint32_t voff[LPT];
 
-  __device__ __forceinline__ void issue(const uint16_t* kb, int64_t kst, int t0, int T, char* tile) const {
+  __device__ __forceinline__ static void slot_of(int i, int& slot0, int& row, int& c) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    slot0 = i * NTHREADS + wave * 64;
+    const int slot = slot0 + lane;
+    row = slot / CPR;
+    c = (slot % CPR) ^ ((kt_off<D>(row, 0) >> 4) - row * CPR);
+  }
+
+  __device__ __forceinline__ void init(int64_t kst) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int slot0 = i * NTHREADS + wave * 64;
-      const int slot = slot0 + lane;
-      const int row = slot / CPR;
-      const int c = (slot % CPR) ^ ((kt_off<D>(row, 0) >> 4) - row * CPR);
-      int t = t0 + row;
-      t = t < T ? t : T - 1;
-      __builtin_amdgcn_global_load_lds(kb + static_cast<int64_t>(t) * kst + c * 8,
-                                       (lds_void*)(tile + slot0 * 16), 16, 0, 0);
+      int slot0, row, c;
+      slot_of(i, slot0, row, c);
+      voff[i] = static_cast<uint32_t>(row * kst * 2 + c * 16);
+    }
+  }
+
+  __device__ __forceinline__ void issue(const uint16_t* kb, int64_t kst, int t0, int T, char* tile) const {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (t0 + TILE_N <= T) {
+      // (The source pointer is passed as uint16_t*: a char* argument to this
+      // builtin makes clang drop the host launch stubs of later instantiations.)
+      const char* base = reinterpret_cast<const char*>(kb + static_cast<int64_t>(t0) * kst);
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        const int slot0 = i * NTHREADS + wave * 64;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint16_t*>(base + voff[i]),
+                                         (lds_void*)(tile + slot0 * 16), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        int slot0, row, c;
+        slot_of(i, slot0, row, c);
+        int t = t0 + row;
+        t = t < T ? t : T - 1;
+        __builtin_amdgcn_global_load_lds(kb + static_cast<int64_t>(t) * kst + c * 8,
+                                         (lds_void*)(tile + slot0 * 16), 16, 0, 0);
+      }
     }
   }
 };
@@ -264,7 +295,8 @@ void indexer_topk_kernel(IndexerArgs a) {
   const uint8_t* mrow =
       MASKED ? a.mask + b * a.msb + static_cast<int64_t>(active ? s : 0) * a.mss : nullptr;
 
-  const KTileLoader<D, TILE_N, NT> ld;
+  KTileLoader<D, TILE_N, NT> ld;
+  ld.init(a.kst);
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
   if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
 
@@ -408,7 +440,8 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
   const uint16_t* kb = a.k + b * a.ksb;
   float* orow = a.scores + b * a.ssb + static_cast<int64_t>(active ? s : 0) * a.sss;
 
-  const KTileLoader<D, TILE_N, NT> ld;
+  KTileLoader<D, TILE_N, NT> ld;
+  ld.init(a.kst);
   const int ntiles = (a.T + TILE_N - 1) / TILE_N;
   if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
   tile_barrier();

@@ -86,6 +86,7 @@ struct WaveSelect {
   static constexpr int E = C / kWave;   // 64-key rows in the buffer
   static constexpr int CMAX = C - 192;  // most keys a compaction keeps
   static_assert(E >= 4 && (E & (E - 1)) == 0, "capacity must be 64 * 2^n, n >= 2");
+  // Capacities above 2048 serve only top_k <= C/2 (the full-width sort would not fit in registers).
 
   uint64_t* buf;        // this wave's private LDS buffer, key at position p = buf[p]
   int n;                // keys held (wave-uniform)
@@ -131,7 +132,8 @@ struct WaveSelect {
     return c;
   }
 
-  __device__ __forceinline__ void compact(int lane) {
+  // Raises the floor so that kk <= n <= cmax (needs n > cmax and kk <= cmax).
+  __device__ __forceinline__ void compact_to(int lane, int kk, int cmax) {
     wave_lds_sync();
     uint64_t v[E];
     uint32_t mx = 0;
@@ -142,10 +144,9 @@ struct WaveSelect {
       mx = key_hi(v[j]) > mx ? key_hi(v[j]) : mx;
     }
     mx = wave_max_u32(mx);
-    const int kk = top_k;
-    const int target = kk + (CMAX - kk) / 4;
+    const int target = kk + (cmax - kk) / 4;
 
-    // Invariant: count(hi >= lo) = c_lo > CMAX and count(hi >= hi_) = c_hi < kk.
+    // Invariant: count(hi >= lo) = c_lo > cmax and count(hi >= hi_) = c_hi < kk.
     uint64_t lo = tau, hi_ = static_cast<uint64_t>(mx) + 1;
     int c_lo = n, c_hi = 0;
     uint64_t P = 0;
@@ -163,12 +164,12 @@ struct WaveSelect {
       step = step < 1 ? 1 : (step > span - 1 ? span - 1 : step);
       const uint32_t mid = static_cast<uint32_t>(lo + step);
       c = count_hi_ge(v, mid);
-      if (c >= kk && c <= CMAX) {
+      if (c >= kk && c <= cmax) {
         P = static_cast<uint64_t>(mid) << 32;
         found = true;
         break;
       }
-      if (c > CMAX) {
+      if (c > cmax) {
         lo = mid;
         c_lo = c;
       } else {
@@ -183,12 +184,12 @@ struct WaveSelect {
       for (int it = 0; it < 64 && phi - plo > 1; ++it) {
         const uint64_t mid = plo + ((phi - plo) >> 1);
         c = count_ge(v, mid);
-        if (c >= kk && c <= CMAX) {
+        if (c >= kk && c <= cmax) {
           P = mid;
           found = true;
           break;
         }
-        if (c > CMAX) plo = mid; else phi = mid;
+        if (c > cmax) plo = mid; else phi = mid;
       }
       if (!found) {  // unreachable for distinct keys; keep the capacity bound
         P = phi;
@@ -213,24 +214,16 @@ struct WaveSelect {
     wave_lds_sync();
   }
 
+  __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, CMAX); }
+
   // Sorted top_k of the row: indices (int64, -1 pad) and scores (fp32, -inf pad).
+  // When top_k fits in half the buffer, the held keys are first cut to at
+  // most C/2 (exactly top_k if more are held) so that only C/2 are sorted.
   __device__ __forceinline__ void finish(int64_t* out_idx, float* out_score, int lane) {
-    wave_lds_sync();
-    if constexpr (E <= 32) {
-      uint64_t v[E];
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        const int pos = j * kWave + lane;
-        v[j] = pos < n ? buf[pos] : 0ull;
-      }
-      wave_sort_desc<E>(v, lane);
-      write_out<E>(v, out_idx, out_score, lane);
-    } else {
-      // Wider buffers are sorted as two halves of 32 keys per lane: the first
-      // half is parked in LDS in rank order, then one half-cleaner + bitonic
-      // merge yields the top C/2 >= top_k.
-      constexpr int HE = E / 2;
-      constexpr int HALF = C / 2;
+    constexpr int HE = E / 2;
+    if (top_k <= C / 2) {
+      if (n > C / 2) compact_to(lane, top_k, top_k);
+      wave_lds_sync();
       uint64_t v[HE];
 #pragma unroll
       for (int j = 0; j < HE; ++j) {
@@ -238,23 +231,19 @@ struct WaveSelect {
         v[j] = pos < n ? buf[pos] : 0ull;
       }
       wave_sort_desc<HE>(v, lane);
-      wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < HE; ++j) buf[lane * HE + j] = v[j];
-#pragma unroll
-      for (int j = 0; j < HE; ++j) {
-        const int pos = HALF + j * kWave + lane;
-        v[j] = pos < n ? buf[pos] : 0ull;
-      }
-      wave_sort_desc<HE>(v, lane);
-      wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < HE; ++j) {
-        const uint64_t a = buf[HALF - 1 - (lane * HE + j)];
-        v[j] = a > v[j] ? a : v[j];
-      }
-      bitonic_level<HE, kWave * HE, kWave * HE, kWave * HE / 2>(v, lane);
       write_out<HE>(v, out_idx, out_score, lane);
+    } else {
+      if constexpr (E <= 32) {
+        wave_lds_sync();
+        uint64_t v[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+          const int pos = j * kWave + lane;
+          v[j] = pos < n ? buf[pos] : 0ull;
+        }
+        wave_sort_desc<E>(v, lane);
+        write_out<E>(v, out_idx, out_score, lane);
+      }
     }
   }
 
