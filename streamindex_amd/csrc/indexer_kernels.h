@@ -240,7 +240,16 @@ struct TopkShape {
   static constexpr int NW = 4;
   static constexpr int TILE_N = 64;
   static constexpr int WAVES_PER_EU = C <= 1024 ? 2 : 1;
+  // K tiles in the LDS ring (a third buffer measured no faster at S = 64K).
+  static constexpr int RING = 2;
 };
+
+// s_waitcnt with vmcnt = n (0..15), lgkmcnt = 0, expcnt not waited (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4));
+}
 
 // ---------------------------------------------------------------------------
 // Fused score + streaming exact top-k.
@@ -258,10 +267,11 @@ void indexer_topk_kernel(IndexerArgs a) {
   constexpr int G = NB * HB;       // MFMA groups per tile (even)
   constexpr int TILE_BYTES = TILE_N * D * 2;
   constexpr int BLK_BYTES = 32 * D * 2;
+  constexpr int RING = TopkShape<C>::RING;
   // The DMA-filled K ring sits first (global_load_lds destinations stay
   // below 64 KiB), then the per-wave selection buffers.
-  __shared__ __attribute__((aligned(16))) char lds[2 * TILE_BYTES + NW * C * 8];
-  uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + 2 * TILE_BYTES);
+  __shared__ __attribute__((aligned(16))) char lds[RING * TILE_BYTES + NW * C * 8];
+  uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + RING * TILE_BYTES);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -298,7 +308,10 @@ void indexer_topk_kernel(IndexerArgs a) {
   KTileLoader<D, TILE_N, NT> ld;
   ld.init(a.kst);
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
-  if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
+  constexpr int LPT = KTileLoader<D, TILE_N, NT>::LPT;  // tile copies per thread
+#pragma unroll
+  for (int i = 0; i < RING - 1; ++i)
+    if (i < ntiles) ld.issue(kb, a.kst, i * TILE_N, a.T, lds + i * TILE_BYTES);
 
   // Pipeline state carried across tiles.  Each of the G groups of a tile has
   // its own accumulator; the epilogue runs LAG = HB groups behind the MFMAs,
@@ -330,16 +343,23 @@ void indexer_topk_kernel(IndexerArgs a) {
     offer_tile(prev_p0, p1, prev_tbase, true, prev_mask);
   };
 
-  tile_barrier();
+  // Tile 0 landed (the copies of tiles 1..RING-2 may still be in flight).
+  if (RING == 3 && ntiles > 1) wait_vm_lgkm0<LPT>(); else wait_vm_lgkm0<0>();
+  __syncthreads();
 
+  int slot = 0;  // ring slot of tile `it`
   for (int it = 0; it < ntiles; ++it) {
-    if (it + 1 < ntiles) ld.issue(kb, a.kst, (it + 1) * TILE_N, a.T, lds + ((it + 1) & 1) * TILE_BYTES);
-    const char* tile = lds + (it & 1) * TILE_BYTES;
     const int tbase = it * TILE_N;
-    if constexpr (MASKED) {
+    if constexpr (MASKED) {  // issued before the tile copies so the waits below cover only the copies
       const int t = tbase + okey;
       cur_mask = t < my_lim ? mrow[static_cast<int64_t>(t) * a.mst] != 0 : false;
     }
+    // The slot of tile it+RING-1 last held tile it-1, which every wave
+    // finished before the barrier that ended the previous iteration.
+    const int fill = slot == 0 ? RING - 1 : slot - 1;
+    const bool more = it + RING - 1 < ntiles;
+    if (more) ld.issue(kb, a.kst, (it + RING - 1) * TILE_N, a.T, lds + fill * TILE_BYTES);
+    const char* tile = lds + slot * TILE_BYTES;
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
 
@@ -406,7 +426,10 @@ void indexer_topk_kernel(IndexerArgs a) {
       }
     }
     if (sel.needs_compaction()) sel.compact(lane);
-    tile_barrier();
+    // Tile it+1 must have landed; the copies of tile it+RING-1 may stay in flight.
+    if (RING == 3 && more) wait_vm_lgkm0<LPT>(); else wait_vm_lgkm0<0>();
+    __syncthreads();
+    slot = slot == RING - 1 ? 0 : slot + 1;
   }
 
   if (pend) drain();

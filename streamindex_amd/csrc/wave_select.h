@@ -27,31 +27,60 @@
 
 namespace si {
 
-// One bitonic compare-exchange stage; rank e = lane*E+j.  SIZE and STRIDE are
-// compile-time so that every register index below is static.
+// Bitonic network over 64*E keys held E per lane, rank e = lane*E + j; a
+// block of SIZE ranks is sorted descending when (e & SIZE) == 0 (or when it
+// is the whole sequence).  Each stage's direction pattern is a compile-time
+// lane mask, so a compare-exchange is one 64-bit compare into a lane mask,
+// one scalar XOR with the constant and the selects.
+
+// Lanes whose keys of a SIZE-block run descending (SIZE >= E: depends on the lane only).
+template <int E, int N, int SIZE>
+constexpr uint64_t desc_lane_mask() {
+  uint64_t m = 0;
+  for (int l = 0; l < kWave; ++l)
+    if (SIZE >= N || ((l * E) & SIZE) == 0) m |= 1ull << l;
+  return m;
+}
+
+// Cross-lane stage, partner lane = lane ^ LX: lanes that keep the larger key.
+template <int E, int N, int SIZE, int LX>
+constexpr uint64_t keep_max_lane_mask() {
+  uint64_t m = 0;
+  for (int l = 0; l < kWave; ++l) {
+    const bool lower = (l & LX) == 0;
+    const bool desc = SIZE >= N || ((l * E) & SIZE) == 0;
+    if (lower == desc) m |= 1ull << l;
+  }
+  return m;
+}
+
 template <int E, int N, int SIZE, int STRIDE>
 __device__ __forceinline__ void bitonic_stage(uint64_t (&v)[E], int lane) {
   if constexpr (STRIDE >= E) {
     constexpr int LX = STRIDE / E;
-    const bool lower = (lane & LX) == 0;
+    constexpr uint64_t KM = keep_max_lane_mask<E, N, SIZE, LX>();
+    uint64_t o[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) o[j] = shfl_xor_u64(v[j], lane, LX);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const int e = lane * E + j;
-      const bool desc = (SIZE >= N) || ((e & SIZE) == 0);
-      const uint64_t o = shfl_xor_u64(v[j], lane, LX);
-      const bool keep_max = (lower == desc);
-      const bool take = keep_max ? (o > v[j]) : (o < v[j]);
-      v[j] = take ? o : v[j];
+      // take the partner's key iff it is larger and this lane keeps the max, or
+      // smaller and this lane keeps the min (equal keys: either choice)
+      const uint64_t gt = __builtin_amdgcn_ballot_w64(o[j] > v[j]);
+      const bool take = __builtin_amdgcn_inverse_ballot_w64(~(gt ^ KM));
+      v[j] = take ? o[j] : v[j];
     }
   } else {
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       if ((j ^ STRIDE) > j) {
         const int p = j ^ STRIDE;
-        const int e = lane * E + j;
-        const bool desc = (SIZE >= N) || ((e & SIZE) == 0);
+        // descending pair: swap when v[j] < v[p]; ascending: when v[j] > v[p]
+        const uint64_t DM = (SIZE >= N) ? ~0ull
+                            : (SIZE >= E ? desc_lane_mask<E, N, SIZE>() : (((j & SIZE) == 0) ? ~0ull : 0ull));
         const uint64_t a = v[j], b = v[p];
-        const bool sw = desc ? (a < b) : (a > b);
+        const uint64_t lt = __builtin_amdgcn_ballot_w64(a < b);
+        const bool sw = __builtin_amdgcn_inverse_ballot_w64(~(lt ^ DM));
         v[j] = sw ? b : a;
         v[p] = sw ? a : b;
       }
@@ -214,7 +243,10 @@ struct WaveSelect {
     wave_lds_sync();
   }
 
-  __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, CMAX); }
+  // Keeping close to top_k keys leaves the most room and the highest floor.
+  __device__ __forceinline__ void compact(int lane) {
+    compact_to(lane, top_k, top_k + 64 < CMAX ? top_k + 64 : CMAX);
+  }
 
   // Sorted top_k of the row: indices (int64, -1 pad) and scores (fp32, -inf pad).
   // When top_k fits in half the buffer, the held keys are first cut to at
