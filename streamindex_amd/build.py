@@ -39,9 +39,18 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source extra flags.  The sparse-attention kernel keeps its MFMA
+# accumulators in VGPRs (not AGPRs): its rare online-softmax rescale multiplies
+# them with VALU, and AGPR-resident accumulators made the compiler copy all of
+# them into VGPRs on every loop iteration.
+EXTRA_FLAGS = {
+    "sparse_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}")

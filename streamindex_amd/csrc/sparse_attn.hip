@@ -9,19 +9,32 @@
 //   p_j = e^{scale·q[s,h]·kv[idx_j] - m},  idx_j = -1 (or out of range) masked,
 //   lse[s,h] = log(Σ_j p_j + e^{sink_h - m}) + m.
 //
-// Design (one query row per workgroup, 16 heads per wavefront):
-//   * The row's top-k KV rows are gathered TK = 32 at a time from HBM/L2 with
-//     16-byte loads (each row read once per query, not once per head block)
-//     and written to LDS twice: key-major (swizzled) for the score MFMAs and
-//     dim-major (transposed in registers) for the P·V MFMAs.
-//   * Scores are computed transposed, S^T = KV·Q^T with
-//     v_mfma_f32_16x16x32_bf16 (keys on M, heads on N), so each lane holds one
-//     head: the online-softmax max/sum stay in-lane plus two xor exchanges.
-//   * O^T = V^T·P^T uses the score accumulators directly as the B operand
-//     (keys permuted consistently in both operands), and its output layout
-//     puts one head per lane again, so the rescale by e^{m_old-m_new} is
-//     lane-local.  Q lives in VGPRs for the whole row.
+// Design (one query row and up to 64 heads per workgroup of 4 waves):
+//   * The row's top-k KV rows are gathered 32 at a time straight from L2/HBM
+//     into a 3-slot LDS ring with global_load_lds (no staging registers), two
+//     tiles ahead of use; each row is read once per query for all heads.
+//     Rows are stored key-major with a per-key XOR swizzle of the 16-byte
+//     chunks so that both LDS read patterns below are bank-conflict-free.
+//   * S^T = K·Q^T (v_mfma_f32_16x16x32_bf16, keys on M, heads on N), split
+//     across the waves by head (16 heads per wave, Q^T in VGPRs).  Each lane
+//     then holds one head, so the online-softmax max and sum are in-lane plus
+//     two xor exchanges.  The reference maximum is raised only when the tile
+//     maximum exceeds it by 2^64 (the result is unchanged up to rounding), so
+//     after the first valid tile the output accumulator is in practice never
+//     rescaled.
+//   * P^T (bf16) and the per-head rescale factors of all 64 heads are
+//     exchanged through a small double-buffered LDS area; one barrier per
+//     tile.
+//   * O^T = V^T·P^T, split across the waves by output dimension (the 16-dim
+//     blocks are dealt round-robin), so every V element is read from LDS once.
+//     The V^T A-fragments are read from the key-major tile with
+//     ds_read_b64_tr_b16 (two transposing reads give a lane 8 keys of one
+//     dimension); the P^T B-fragments use the key order of the score
+//     accumulators, so no register shuffles are needed.
+//   * The normalised output is staged through LDS and written with
+//     coalesced 16-byte stores.
 #include <string>
+#include <type_traits>
 
 #include "si_common.h"
 #include "si_status.h"
@@ -42,23 +55,91 @@ struct SparseAttnArgs {
   float* lse;          // [B,S,H]
   int64_t lsb, lss, lsh;
   int B, S, H, N, K;
+  int HG;              // head groups of 64
   float scale_log2;    // softmax_scale * log2(e)
 };
 
-constexpr int kTK = 32;  // keys per tile
+constexpr int kAttnTK = 32;      // keys per tile
+constexpr int kAttnWaves = 4;    // waves per workgroup; 16 heads each in S^T
+constexpr int kAttnRing = 3;     // KV tiles resident in LDS
+// The reference maximum of a head moves only when a tile's maximum exceeds it
+// by 2^64 (log2 units): p = 2^(x - m_ref) then stays below 2^64, far inside
+// the fp32/bf16 exponent range, and the output accumulator is rescaled only
+// on such a jump.  (Up to rounding the result equals the eager rescale.)
+constexpr float kLazyRescale = 64.0f;
 
 template <int D>
-__device__ __forceinline__ int kmaj_off(int key, int c) {
-  constexpr int CPR = D / 8;
-  constexpr int SW = CPR < 8 ? CPR : 8;
-  return key * (D * 2) + ((c ^ (key % SW)) << 4);
+struct AttnShape {
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per KV row
+  static constexpr int ROW = D * 2;                  // bytes per KV row
+  static constexpr int TILE = kAttnTK * ROW;         // bytes per KV tile
+  static constexpr int CH = kAttnTK * CPR;           // chunks per tile
+  static constexpr int NT = kAttnWaves * 64;
+  static constexpr int LPT = (CH + NT - 1) / NT;     // tile copies per thread
+  static constexpr int KS = D / 32;                  // S^T k-steps
+  static constexpr int MBT = D / 16;                 // 16-dim output blocks
+  static constexpr int MBW = (MBT + kAttnWaves - 1) / kAttnWaves;  // per wave
+  static constexpr int OROW = ROW + 16;              // staged output row (padded)
+  static constexpr int OUT = 64 * OROW;              // staged output bytes
+  static constexpr int LDS_KV = (kAttnRing * TILE > OUT) ? kAttnRing * TILE : OUT;
+  static constexpr int FMASK = CPR >= 8 ? 7 : 0;     // chunk swizzle width
+};
+
+// Chunk swizzle of key row k: f(k) = ((k & 3) << 1) | ((k >> 2) & 1).  With
+// 32 four-byte banks (128 bytes per LDS cycle) it makes the 8 keys read at one
+// chunk by an 8-lane ds_read_b128 phase, and the 4 keys x 2 chunks read by a
+// 16-lane ds_read_b64_tr_b16 phase, occupy distinct 16-byte bank groups.
+template <int D>
+__device__ __forceinline__ int kv_swz(int k) {
+  return (((k & 3) << 1) | ((k >> 2) & 1)) & AttnShape<D>::FMASK;
+}
+template <int D>
+__device__ __forceinline__ int kv_off(int k, int c) {
+  return k * (D * 2) + ((c ^ kv_swz<D>(k)) << 4);
 }
 
-// V^T rows hold kTK keys (64 bytes) padded to 72 bytes to stagger banks.
-constexpr int kVRow = kTK * 2 + 8;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const char lds_cchar;
 
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cchar*)p));
+}
+
+// ds_read_b64_tr_b16 issued from inline asm at LDS byte address addr + OFF.
+// Through the builtin, the compiler makes every such read wait for all
+// outstanding LDS-DMA copies (vmcnt(0)), which would serialise the gather of
+// later tiles with this tile's P.V; issued this way the read is ordered only
+// by lds_wait below.
+template <int OFF>
+__device__ __forceinline__ v4i16 tr_read(uint32_t addr) {
+  v4i16 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+
+// ds_read_b128 at LDS byte address addr + OFF, issued in program order (the
+// compiler would otherwise move each read next to its use and serialise the
+// S^T MFMAs behind the LDS latency).
+template <int OFF>
+__device__ __forceinline__ bf16x8 ld128(uint32_t addr) {
+  bf16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+
+// Waits until at most N of this wave's LDS operations are outstanding.  The
+// two registers are tied to the wait so that their uses stay after it.  LDS
+// operations complete in order, so the compiler's own lgkmcnt waits stay
+// correct (they only become stricter) with these reads in flight.
+template <int N>
+__device__ __forceinline__ void lds_wait(v4i16& x, v4i16& y) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(bf16x8& x, bf16x8& y) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
+}
 
 __device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
   // round-to-nearest-even to bf16 (finite values)
@@ -68,188 +149,341 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
   return ua | (ub << 16);
 }
 
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int I, int N, typename F>
+__device__ __forceinline__ void attn_static_for(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    attn_static_for<I + 1, N>(f);
+  }
+}
+
 template <int D>
-__global__ __launch_bounds__(512) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
-  constexpr int KS = D / 32;  // k-steps of the score MFMA
-  constexpr int MD = D / 16;  // 16-dim blocks of the output MFMA
-  constexpr int CPR = D / 8;
-  __shared__ __attribute__((aligned(16))) char kmaj[kTK * D * 2];
-  __shared__ __attribute__((aligned(16))) char vt[D * kVRow];
-  __shared__ int sidx[kTK];
+__global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
+  using SH = AttnShape<D>;
+  constexpr int KS = SH::KS;
+  constexpr int MBW = SH::MBW;
+  constexpr int ROW = SH::ROW;
+  __shared__ __attribute__((aligned(16))) char kv_lds[SH::LDS_KV];
+  __shared__ __attribute__((aligned(16))) char p_lds[2][kAttnWaves * 64 * 16];  // P^T B-fragments per head block
+  __shared__ float alpha_lds[2][64];
+  __shared__ float scale_lds[64];
+  __shared__ __attribute__((aligned(16))) int valid_lds[kAttnRing][kAttnTK];  // 1 = key used
+  __shared__ int64_t rowoff_lds[kAttnRing][kAttnTK];     // byte offset of the key's KV row
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __builtin_assume(wave >= 0 && wave < kAttnWaves);
   const int g = lane >> 4;     // lane group 0..3
-  const int hl = lane & 15;    // head within the wave's 16
-  const int nthreads = blockDim.x;
+  const int i16 = lane & 15;
   const int s = blockIdx.x % a.S;
-  const int b = blockIdx.x / a.S;
-  const int h = wave * 16 + hl;
-  const bool hvalid = h < a.H;
-
-  // Q^T B-fragments: head h, dims 32ks + 8g .. +8.
-  bf16x8 qf[KS];
-  {
-    const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(h) * a.qsh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
-    }
-  }
-
-  f32x4 acc[MD];
-#pragma unroll
-  for (int md = 0; md < MD; ++md) acc[md] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -1.0e30f;  // running max (log2 domain), one head per lane
-  float l_run = 0.f;       // this lane's share of the running denominator
+  const int rest = blockIdx.x / a.S;
+  const int b = rest % a.B;
+  const int hg = rest / a.B;
+  const int hbase = hg * 64;
+  const int hq = hbase + wave * 16 + i16;  // this lane's head in S^T
+  const bool hvalid = hq < a.H;
+  const int ntiles = (a.K + kAttnTK - 1) / kAttnTK;
 
   const char* idx_row = static_cast<const char*>(a.idx) +
                         (b * a.isb + static_cast<int64_t>(s) * a.iss) * (a.idx64 ? 8 : 4);
-  const uint16_t* kvb = a.kv + b * a.kvsb;
-  const int ntiles = (a.K + kTK - 1) / kTK;
+  const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+
+  // Key indices of tile `t` (wave 0; lane l reads key l % 32).  The raw words
+  // are kept in a register and widened and published to ring slot t % 3 one
+  // iteration later, so the load is never waited for right after issue.
+  auto load_idx = [&](int t, uint2& raw) {
+    int j = t * kAttnTK + (lane & 31);
+    j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
+    const int64_t off = static_cast<int64_t>(j) * a.isk;
+    if (a.idx64) {
+      raw = reinterpret_cast<const uint2*>(idx_row)[off];
+    } else {
+      raw.x = reinterpret_cast<const uint32_t*>(idx_row)[off];
+    }
+  };
+  auto store_idx = [&](int t, uint2 w) {
+    const int64_t raw = a.idx64 ? static_cast<int64_t>((static_cast<uint64_t>(w.y) << 32) | w.x)
+                                : static_cast<int64_t>(static_cast<int32_t>(w.x));
+    const int slot = t % kAttnRing;
+    const int j = t * kAttnTK + lane;
+    const bool ok = j < a.K && raw >= 0 && raw < a.N;
+    if (lane < kAttnTK) {
+      valid_lds[slot][lane] = ok;
+      rowoff_lds[slot][lane] = (ok ? raw : 0) * a.kvsn * 2;
+    }
+  };
+  // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
+  // holds chunk (e % CPR) ^ f(key) of key e / CPR.  Needs N > 0.  This
+  // thread's (key, chunk byte offset) per copy are fixed, computed once.
+  int dkey[SH::LPT], dcoff[SH::LPT];
+#pragma unroll
+  for (int i = 0; i < SH::LPT; ++i) {
+    const int e = i * SH::NT + static_cast<int>(threadIdx.x);
+    dkey[i] = e / SH::CPR;
+    dcoff[i] = ((e % SH::CPR) ^ kv_swz<D>(dkey[i])) * 16;
+  }
+  auto issue_tile = [&](int t) {
+    const int slot = t % kAttnRing;
+    char* dst = kv_lds + slot * SH::TILE;
+#pragma unroll
+    for (int i = 0; i < SH::LPT; ++i) {
+      const int e0 = i * SH::NT + wave * 64;
+      if (e0 < SH::CH) {
+        // (passed as uint16_t*: a char* argument to this builtin makes clang
+        // drop the host launch stubs of later instantiations)
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + rowoff_lds[slot][dkey[i]] + dcoff[i]);
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst + e0 * 16), 16, 0, 0);
+      }
+    }
+  };
+
+  // Ring protocol: tile t lives in slot t % 3.  Iteration `it` consumes tile
+  // `it`; its one barrier (after the P^T exchange) is preceded by a full wait
+  // for the gather of tile it+1 and followed by the gather of tile it+2 into
+  // the slot of tile it-1, whose P.V every wave has finished by then.
+
+  // ---- prologue: Q^T fragments, indices of tiles 0..2, gathers of tiles 0..1 ----
+  bf16x8 qf[KS];
+  {
+    const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
+  }
+  const bool has_kv = a.N > 0;
+  uint2 nidx = {0u, 0u};
+  if (wave == 0 && ntiles > 0) {
+    uint2 r0 = {0u, 0u}, r1 = {0u, 0u};
+    load_idx(0, r0);
+    if (ntiles > 1) load_idx(1, r1);
+    if (ntiles > 2) load_idx(2, nidx);
+    store_idx(0, r0);
+    if (ntiles > 1) store_idx(1, r1);
+  }
+  __syncthreads();
+  if (has_kv) {
+    if (ntiles > 0) issue_tile(0);
+    if (ntiles > 1) issue_tile(1);
+  }
+  // tile 0 landed; the gather of tile 1 may still be in flight
+  if (ntiles > 1 && has_kv) __builtin_amdgcn_s_waitcnt((SH::LPT & 0xF) | (0x7 << 4));
+  else __builtin_amdgcn_s_waitcnt(0x7 << 4);
+  __syncthreads();
+
+  // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
+  // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
+  // offset is a per-lane base (one per ks parity) plus 64 ks + 16 ROW mb.
+  const int qf_swz = kv_swz<D>(i16);
+  const int qbase = i16 * ROW + 16 * (g ^ (qf_swz & 3));
+  const int qadj = 64 * (qf_swz >> 2);
+  // V^T transposing-read address: source lane (g, i16) points at key
+  // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
+  // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
+  // swizzles to 8j + (x ^ f), so block j is at a fixed base + 128 j.
+  const int tkey = 4 * g + (i16 >> 2);
+  const int tx = 2 * wave + ((i16 & 3) >> 1);
+  const int tbase = tkey * ROW + 16 * ((tx ^ kv_swz<D>(tkey)) & (SH::CPR - 1)) + 8 * (i16 & 1);
+
+  f32x4 oacc[MBW][4];
+#pragma unroll
+  for (int j = 0; j < MBW; ++j)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
+  float l_run = 0.f;       // this lane's share of the denominator
 
   for (int it = 0; it < ntiles; ++it) {
-    const int k0 = it * kTK;
-    if (threadIdx.x < kTK) {
-      const int j = k0 + threadIdx.x;
-      int t = -1;
-      if (j < a.K) {
-        const int64_t off = static_cast<int64_t>(j) * a.isk;
-        const int64_t v = a.idx64 ? reinterpret_cast<const int64_t*>(idx_row)[off]
-                                  : static_cast<int64_t>(reinterpret_cast<const int32_t*>(idx_row)[off]);
-        t = (v >= 0 && v < a.N) ? static_cast<int>(v) : -1;
-      }
-      sidx[threadIdx.x] = t;
-    }
-    __syncthreads();
+    const int slot = it % kAttnRing;
+    const char* tile = kv_lds + slot * SH::TILE;
 
-    // Gather: block = 4 keys x 8 dims; key-major copy + transposed copy.
-    for (int blk = threadIdx.x; blk < (kTK / 4) * CPR; blk += nthreads) {
-      const int kg = blk / CPR, c = blk % CPR;
-      u32x4 r[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = sidx[kg * 4 + j];
-        r[j] = t >= 0 ? *reinterpret_cast<const u32x4*>(kvb + static_cast<int64_t>(t) * a.kvsn + c * 8)
-                      : u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(kmaj + kmaj_off<D>(kg * 4 + j, c)) = r[j];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // dims c*8 + 2e (low halves) and c*8 + 2e + 1 (high halves)
-        uint2 lo2, hi2;
-        lo2.x = pack_lo(r[0][e], r[1][e]);
-        lo2.y = pack_lo(r[2][e], r[3][e]);
-        hi2.x = pack_hi(r[0][e], r[1][e]);
-        hi2.y = pack_hi(r[2][e], r[3][e]);
-        *reinterpret_cast<uint2*>(vt + (c * 8 + 2 * e) * kVRow + kg * 8) = lo2;
-        *reinterpret_cast<uint2*>(vt + (c * 8 + 2 * e + 1) * kVRow + kg * 8) = hi2;
-      }
-    }
-    __syncthreads();
+    // ---- S^T = K Q^T for this wave's 16 heads: keys 16mb + 4g + r --------
+    // A-fragments stream through a QPD-deep register queue: each MFMA's
+    // operand was read from LDS QPD k-steps earlier.
+    constexpr int QPD = KS < 4 ? KS : 4;
+    const uint32_t qa_e = lds_addr(tile) + qbase + qadj;
+    const uint32_t qa_o = lds_addr(tile) + qbase - qadj;
+    bf16x8 kq[QPD][2];
+    auto qk_issue = [&](auto KC) {
+      constexpr int ks = decltype(KC)::value;
+      const uint32_t base = (ks & 1) ? qa_o : qa_e;
+      kq[ks % QPD][0] = ld128<64 * ks>(base);
+      kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+    };
+    attn_static_for<0, QPD>(qk_issue);
+    f32x4 st[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    auto qk_step = [&](auto KC) {
+      constexpr int ks = decltype(KC)::value;
+      constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
+      lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
+      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
+      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
+      if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
+    };
+    attn_static_for<0, KS>(qk_step);
 
-    // S^T = KV_tile · Q^T : keys 16mb + 4g + i, head hl.
-    f32x4 st[2];
-    st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- online softmax for head hq ---------------------------------------
+    const int4 v0 = *reinterpret_cast<const int4*>(&valid_lds[slot][4 * g]);
+    const int4 v1 = *reinterpret_cast<const int4*>(&valid_lds[slot][16 + 4 * g]);
+    float x[2][4];
+    x[0][0] = v0.x ? st[0][0] * a.scale_log2 : -__builtin_inff();
+    x[0][1] = v0.y ? st[0][1] * a.scale_log2 : -__builtin_inff();
+    x[0][2] = v0.z ? st[0][2] * a.scale_log2 : -__builtin_inff();
+    x[0][3] = v0.w ? st[0][3] * a.scale_log2 : -__builtin_inff();
+    x[1][0] = v1.x ? st[1][0] * a.scale_log2 : -__builtin_inff();
+    x[1][1] = v1.y ? st[1][1] * a.scale_log2 : -__builtin_inff();
+    x[1][2] = v1.z ? st[1][2] * a.scale_log2 : -__builtin_inff();
+    x[1][3] = v1.w ? st[1][3] * a.scale_log2 : -__builtin_inff();
+    float tmax = -__builtin_inff();
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kmaj + kmaj_off<D>(mb * 16 + hl, ks * 4 + g));
-        st[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], st[mb], 0, 0, 0);
-      }
-    }
-
-    float tmax = -1.0e30f;
-    float sv[2][4];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool valid = sidx[mb * 16 + g * 4 + i] >= 0;
-        const float x = valid ? st[mb][i] * a.scale_log2 : -__builtin_inff();
-        sv[mb][i] = x;
-        tmax = __builtin_fmaxf(tmax, x);
-      }
-    }
+      for (int r = 0; r < 4; ++r) tmax = __builtin_fmaxf(tmax, x[mb][r]);
     tmax = __builtin_fmaxf(tmax, shfl_xor_f32(tmax, lane, 16));
     tmax = __builtin_fmaxf(tmax, shfl_xor_f32(tmax, lane, 32));
-    const float m_new = __builtin_fmaxf(m_run, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-
-    float psum = 0.f;
+    // First valid key of the head: the accumulator and denominator are still
+    // zero, so the reference moves without a rescale (alpha = 1).
+    const bool first = m_ref == -1.0e30f;
+    const bool raise = first ? tmax > m_ref : tmax > m_ref + kLazyRescale;
+    const float m_new = raise ? tmax : m_ref;
+    const float alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
+    m_ref = m_new;
     float p[2][4];
+    float psum = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[mb][i] = __builtin_amdgcn_exp2f(sv[mb][i] - m_new);
-        psum += p[mb][i];
+      for (int r = 0; r < 4; ++r) {
+        p[mb][r] = __builtin_amdgcn_exp2f(x[mb][r] - m_new);
+        psum += p[mb][r];
       }
-    }
     l_run = l_run * alpha + psum;
-
-    // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3.
-    bf16x8 pf;
     {
+      // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
       u32x4 w;
       w[0] = f32x2_to_bf16x2(p[0][0], p[0][1]);
       w[1] = f32x2_to_bf16x2(p[0][2], p[0][3]);
       w[2] = f32x2_to_bf16x2(p[1][0], p[1][1]);
       w[3] = f32x2_to_bf16x2(p[1][2], p[1][3]);
-      pf = __builtin_bit_cast(bf16x8, w);
+      *reinterpret_cast<u32x4*>(&p_lds[it & 1][(wave * 64 + lane) * 16]) = w;
+      if (g == 0) alpha_lds[it & 1][wave * 16 + i16] = alpha;
     }
-
-    // O^T[dims, heads] = alpha * O^T + V^T · P^T
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      const char* vrow = vt + (md * 16 + hl) * kVRow;
-      const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + g * 8);
-      const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 32 + g * 8);
-      u32x4 vw;
-      vw[0] = v0.x; vw[1] = v0.y; vw[2] = v1.x; vw[3] = v1.y;
-      const bf16x8 vf = __builtin_bit_cast(bf16x8, vw);
-      acc[md] = acc[md] * alpha;
-      acc[md] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, acc[md], 0, 0, 0);
-    }
+    // indices of tile it+2 (read one iteration ago) are published with P^T
+    if (wave == 0 && it + 2 < ntiles) store_idx(it + 2, nidx);
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // gather of tile it+1 and this wave's LDS traffic done
     __syncthreads();
+    // index load first: a later wait for it then never covers the gather
+    if (wave == 0 && it + 3 < ntiles) load_idx(it + 3, nidx);
+    if (has_kv && it + 2 < ntiles) issue_tile(it + 2);
+
+    // ---- O^T += V^T P^T for this wave's 16-dim blocks, all 64 heads -------
+    float al[4];
+    bf16x8 pb[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+      pb[nb] = *reinterpret_cast<const bf16x8*>(&p_lds[it & 1][(nb * 64 + lane) * 16]);
+    }
+    const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
+                                                         al[3] != 1.0f) != 0;
+    if (__builtin_expect(any_rescale, 0)) {
+#pragma unroll
+      for (int j = 0; j < MBW; ++j)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
+    }
+    const uint32_t ta = lds_addr(tile) + tbase;
+    if constexpr (SH::MBT % kAttnWaves == 0) {
+      // every wave owns MBW blocks; the reads of blocks j+1 and j+2 are in
+      // flight while block j's MFMAs run
+      v4i16 lo[3], hi[3];
+      lo[0] = tr_read<0>(ta);
+      hi[0] = tr_read<16 * ROW>(ta);
+      if constexpr (MBW > 1) {
+        lo[1] = tr_read<128>(ta);
+        hi[1] = tr_read<16 * ROW + 128>(ta);
+      }
+      auto step = [&](auto JC) {
+        constexpr int j = decltype(JC)::value;
+        if constexpr (j + 2 < MBW) {
+          lo[(j + 2) % 3] = tr_read<128 * (j + 2)>(ta);
+          hi[(j + 2) % 3] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
+          lds_wait<4>(lo[j % 3], hi[j % 3]);
+        } else if constexpr (j + 1 < MBW) {
+          lds_wait<2>(lo[j % 3], hi[j % 3]);
+        } else {
+          lds_wait<0>(lo[j % 3], hi[j % 3]);
+        }
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j % 3], hi[j % 3], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[j][nb], 0, 0, 0);
+      };
+      attn_static_for<0, MBW>(step);
+    } else {
+      // fewer 16-dim blocks than waves (D = 32): waves past the last block idle
+      if (wave < SH::MBT) {
+        v4i16 lo = tr_read<0>(ta);
+        v4i16 hi = tr_read<16 * ROW>(ta);
+        lds_wait<0>(lo, hi);
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          oacc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[0][nb], 0, 0, 0);
+      }
+    }
   }
 
-  // Finish: total denominator over the four lane groups, then the sink.
+  // ---- finish: denominators, sink, normalisation, lse ---------------------
   float l_tot = l_run + shfl_xor_f32(l_run, lane, 16);
   l_tot = l_tot + shfl_xor_f32(l_tot, lane, 32);
   constexpr float kLog2e = 1.4426950408889634f;
-  const float sink2 = hvalid ? a.sink[h] * kLog2e : -__builtin_inff();
-  const float m_fin = __builtin_fmaxf(m_run, sink2);
-  const float resc = __builtin_amdgcn_exp2f(m_run - m_fin);
+  const float sink2 = hvalid ? a.sink[hq] * kLog2e : -__builtin_inff();
+  const float m_fin = __builtin_fmaxf(m_ref, sink2);
+  const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
   const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
-  const float inv = l_fin > 0.f ? resc / l_fin : 0.f;
-
-  if (hvalid) {
-    uint16_t* orow = a.o + b * a.osb + static_cast<int64_t>(s) * a.oss + static_cast<int64_t>(h) * a.osh;
-#pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      uint2 w;
-      w.x = f32x2_to_bf16x2(acc[md][0] * inv, acc[md][1] * inv);
-      w.y = f32x2_to_bf16x2(acc[md][2] * inv, acc[md][3] * inv);
-      *reinterpret_cast<uint2*>(orow + md * 16 + g * 4) = w;
-    }
-    if (g == 0) {
+  const float scale = l_fin > 0.f ? resc / l_fin : 0.f;
+  if (g == 0) {
+    scale_lds[wave * 16 + i16] = scale;
+    if (hvalid) {
       constexpr float kLn2 = 0.6931471805599453f;
       const float lse = l_fin > 0.f ? (__builtin_amdgcn_logf(l_fin) + m_fin) * kLn2 : -1.0e30f;
-      a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(h) * a.lsh] = lse;
+      a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(hq) * a.lsh] = lse;
     }
+  }
+  __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
+  __syncthreads();
+  // Normalised O (bf16) staged head-major in LDS: [64 heads][OROW bytes].
+  float sc[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) sc[nb] = scale_lds[nb * 16 + i16];
+#pragma unroll
+  for (int j = 0; j < MBW; ++j) {
+    const int mbi = j * kAttnWaves + wave;
+    if (SH::MBT % kAttnWaves == 0 || mbi < SH::MBT) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        uint2 w;
+        w.x = f32x2_to_bf16x2(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
+        w.y = f32x2_to_bf16x2(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
+        *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
+      }
+    }
+  }
+  __syncthreads();
+  const int hcount = (a.H - hbase) < 64 ? (a.H - hbase) : 64;
+  uint16_t* obase = a.o + b * a.osb + static_cast<int64_t>(s) * a.oss + static_cast<int64_t>(hbase) * a.osh;
+  for (int e = threadIdx.x; e < hcount * SH::CPR; e += SH::NT) {
+    const int h = e / SH::CPR, c = e % SH::CPR;
+    *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(h) * a.osh + c * 8) =
+        *reinterpret_cast<const u32x4*>(kv_lds + h * SH::OROW + c * 16);
   }
 }
 
 template <int D>
 static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
-  const int nw = (a.H + 15) / 16;
-  const int64_t nblk = static_cast<int64_t>(a.B) * a.S;
+  const int64_t nblk = static_cast<int64_t>(a.B) * a.S * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D>), dim3(static_cast<unsigned>(nblk)), dim3(nw * 64), 0, st, a);
+  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64), 0, st, a);
   return check_launch("sparse_attn_fwd_kernel");
 }
 
@@ -276,10 +510,10 @@ extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const
     return set_error(SI_ERR_INVALID, "q, kv and o need a contiguous last dimension");
   if ((q_strides[0] | q_strides[1] | q_strides[2] | kv_strides[0] | kv_strides[1]) % 8)
     return set_error(SI_ERR_INVALID, "q/kv strides must be multiples of 8 elements");
-  if ((o_strides[0] | o_strides[1] | o_strides[2]) % 4) return set_error(SI_ERR_INVALID, "o strides must be multiples of 4");
+  if ((o_strides[0] | o_strides[1] | o_strides[2]) % 8) return set_error(SI_ERR_INVALID, "o strides must be multiples of 8");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kv)) & 15)
     return set_error(SI_ERR_INVALID, "q/kv must be 16-byte aligned");
-  if (reinterpret_cast<uintptr_t>(o) & 7) return set_error(SI_ERR_INVALID, "o must be 8-byte aligned");
+  if (reinterpret_cast<uintptr_t>(o) & 15) return set_error(SI_ERR_INVALID, "o must be 16-byte aligned");
   SparseAttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
@@ -295,6 +529,7 @@ extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const
   a.lsb = lse_strides[0]; a.lss = lse_strides[1]; a.lsh = lse_strides[2];
   a.B = static_cast<int>(B); a.S = static_cast<int>(S); a.H = static_cast<int>(H);
   a.N = static_cast<int>(N_kv); a.K = static_cast<int>(K);
+  a.HG = static_cast<int>((H + 63) / 64);
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   if (a.B == 0 || a.S == 0) return SI_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
