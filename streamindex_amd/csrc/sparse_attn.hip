@@ -85,13 +85,14 @@ struct AttnShape {
   static constexpr int FMASK = CPR >= 8 ? 7 : 0;     // chunk swizzle width
 };
 
-// Chunk swizzle of key row k: f(k) = ((k & 3) << 1) | ((k >> 2) & 1).  With
-// 32 four-byte banks (128 bytes per LDS cycle) it makes the 8 keys read at one
-// chunk by an 8-lane ds_read_b128 phase, and the 4 keys x 2 chunks read by a
-// 16-lane ds_read_b64_tr_b16 phase, occupy distinct 16-byte bank groups.
+// Chunk swizzle of key row k: chunk c is stored at c ^ (k & 7).  Measured on
+// gfx950 (SQ_LDS_BANK_CONFLICT), this makes both read patterns below
+// conflict-free: the S^T A-fragment ds_read_b128 (16 keys at one chunk per
+// quarter-wave) and the V^T ds_read_b64_tr_b16 (4 keys x 32 bytes per
+// 16-lane group).  The row stride alone (1152 bytes) gives 4-way conflicts.
 template <int D>
 __device__ __forceinline__ int kv_swz(int k) {
-  return (((k & 3) << 1) | ((k >> 2) & 1)) & AttnShape<D>::FMASK;
+  return k & AttnShape<D>::FMASK;
 }
 template <int D>
 __device__ __forceinline__ int kv_off(int k, int c) {
@@ -158,7 +159,7 @@ __device__ __forceinline__ void attn_static_for(F& f) {
   }
 }
 
-template <int D>
+template <int D, bool IDX64>
 __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
   using SH = AttnShape<D>;
   constexpr int KS = SH::KS;
@@ -170,6 +171,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   __shared__ float scale_lds[64];
   __shared__ __attribute__((aligned(16))) int valid_lds[kAttnRing][kAttnTK];  // 1 = key used
   __shared__ int64_t rowoff_lds[kAttnRing][kAttnTK];     // byte offset of the key's KV row
+  __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[kAttnRing][2 * kAttnTK];  // raw index words
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -186,29 +188,30 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   const int ntiles = (a.K + kAttnTK - 1) / kAttnTK;
 
   const char* idx_row = static_cast<const char*>(a.idx) +
-                        (b * a.isb + static_cast<int64_t>(s) * a.iss) * (a.idx64 ? 8 : 4);
+                        (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
   const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
 
-  // Key indices of tile `t` (wave 0; lane l reads key l % 32).  The raw words
-  // are kept in a register and widened and published to ring slot t % 3 one
-  // iteration later, so the load is never waited for right after issue.
-  auto load_idx = [&](int t, uint2& raw) {
-    int j = t * kAttnTK + (lane & 31);
+  // Key indices of tile `t`: wave 0 copies the raw index words into
+  // idxraw_lds[t % 3] with a global_load_lds (nothing lands in registers, so
+  // no loop-carried load result forces an early wait), and after its next
+  // full wait reads them back, validates them and publishes validity and row
+  // byte offsets to ring slot t % 3 for every wave.
+  auto load_idx = [&](int t) {
+    // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
+    int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
     j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
-    const int64_t off = static_cast<int64_t>(j) * a.isk;
-    if (a.idx64) {
-      raw = reinterpret_cast<const uint2*>(idx_row)[off];
-    } else {
-      raw.x = reinterpret_cast<const uint32_t*>(idx_row)[off];
-    }
+    const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
+                                     (lds_void_t*)(&idxraw_lds[t % kAttnRing][0]), 4, 0, 0);
   };
-  auto store_idx = [&](int t, uint2 w) {
-    const int64_t raw = a.idx64 ? static_cast<int64_t>((static_cast<uint64_t>(w.y) << 32) | w.x)
-                                : static_cast<int64_t>(static_cast<int32_t>(w.x));
+  auto store_idx = [&](int t) {
     const int slot = t % kAttnRing;
-    const int j = t * kAttnTK + lane;
-    const bool ok = j < a.K && raw >= 0 && raw < a.N;
     if (lane < kAttnTK) {
+      const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[slot][2 * lane + 1]) << 32) |
+                                                       idxraw_lds[slot][2 * lane])
+                                : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[slot][lane]));
+      const int j = t * kAttnTK + lane;
+      const bool ok = j < a.K && raw >= 0 && raw < a.N;
       valid_lds[slot][lane] = ok;
       rowoff_lds[slot][lane] = (ok ? raw : 0) * a.kvsn * 2;
     }
@@ -226,13 +229,18 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   auto issue_tile = [&](int t) {
     const int slot = t % kAttnRing;
     char* dst = kv_lds + slot * SH::TILE;
+    // all row offsets first, so the copies are not serialised behind LDS reads
+    int64_t roff[SH::LPT];
+#pragma unroll
+    for (int i = 0; i < SH::LPT; ++i) roff[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] : 0;
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < SH::LPT; ++i) {
       const int e0 = i * SH::NT + wave * 64;
       if (e0 < SH::CH) {
         // (passed as uint16_t*: a char* argument to this builtin makes clang
         // drop the host launch stubs of later instantiations)
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + rowoff_lds[slot][dkey[i]] + dcoff[i]);
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + roff[i] + dcoff[i]);
         __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst + e0 * 16), 16, 0, 0);
       }
     }
@@ -251,14 +259,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     for (int ks = 0; ks < KS; ++ks) qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
   }
   const bool has_kv = a.N > 0;
-  uint2 nidx = {0u, 0u};
   if (wave == 0 && ntiles > 0) {
-    uint2 r0 = {0u, 0u}, r1 = {0u, 0u};
-    load_idx(0, r0);
-    if (ntiles > 1) load_idx(1, r1);
-    if (ntiles > 2) load_idx(2, nidx);
-    store_idx(0, r0);
-    if (ntiles > 1) store_idx(1, r1);
+    load_idx(0);
+    if (ntiles > 1) load_idx(1);
+    if (ntiles > 2) load_idx(2);
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);
+    store_idx(0);
+    if (ntiles > 1) store_idx(1);
   }
   __syncthreads();
   if (has_kv) {
@@ -338,8 +345,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) tmax = __builtin_fmaxf(tmax, x[mb][r]);
-    tmax = __builtin_fmaxf(tmax, shfl_xor_f32(tmax, lane, 16));
-    tmax = __builtin_fmaxf(tmax, shfl_xor_f32(tmax, lane, 32));
+    {  // max over the four lane groups (xor 16, xor 32) with permlane swaps
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
+      tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+    }
     // First valid key of the head: the accumulator and denominator are still
     // zero, so the reference moves without a rescale (alpha = 1).
     const bool first = m_ref == -1.0e30f;
@@ -367,13 +378,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
       *reinterpret_cast<u32x4*>(&p_lds[it & 1][(wave * 64 + lane) * 16]) = w;
       if (g == 0) alpha_lds[it & 1][wave * 16 + i16] = alpha;
     }
-    // indices of tile it+2 (read one iteration ago) are published with P^T
-    if (wave == 0 && it + 2 < ntiles) store_idx(it + 2, nidx);
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // gather of tile it+1 and this wave's LDS traffic done
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // gather of tile it+1, indices of tile it+2, LDS traffic done
+    // indices of tile it+2 (copied one iteration ago) are published with P^T
+    if (wave == 0 && it + 2 < ntiles) store_idx(it + 2);
     __syncthreads();
-    // index load first: a later wait for it then never covers the gather
-    if (wave == 0 && it + 3 < ntiles) load_idx(it + 3, nidx);
     if (has_kv && it + 2 < ntiles) issue_tile(it + 2);
+    if (wave == 0 && it + 3 < ntiles) load_idx(it + 3);
 
     // ---- O^T += V^T P^T for this wave's 16-dim blocks, all 64 heads -------
     float al[4];
@@ -434,8 +444,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   }
 
   // ---- finish: denominators, sink, normalisation, lse ---------------------
-  float l_tot = l_run + shfl_xor_f32(l_run, lane, 16);
-  l_tot = l_tot + shfl_xor_f32(l_tot, lane, 32);
+  float l_tot;
+  {  // sum over the four lane groups
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_tot = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const SwapPair r32 = permlane32_swap(__float_as_uint(l_tot), __float_as_uint(l_tot));
+    l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
+  }
   constexpr float kLog2e = 1.4426950408889634f;
   const float sink2 = hvalid ? a.sink[hq] * kLog2e : -__builtin_inff();
   const float m_fin = __builtin_fmaxf(m_ref, sink2);
@@ -483,7 +498,13 @@ template <int D>
 static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
   const int64_t nblk = static_cast<int64_t>(a.B) * a.S * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((sparse_attn_fwd_kernel<D>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64), 0, st, a);
+  if (a.idx64) {
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64),
+                       0, st, a);
+  } else {
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64),
+                       0, st, a);
+  }
   return check_launch("sparse_attn_fwd_kernel");
 }
 
