@@ -142,17 +142,26 @@ __device__ __forceinline__ void lds_wait(bf16x8& x, bf16x8& y) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// A VALU instruction may read the result of a v_mfma only after the MFMA's
+// wait states (11 for an 8-pass XDL op).  The compiler does not count them
+// when the first read lands in a successor block (here: after the rescale
+// branch), so accumulators that VALU reads go through this fence: 20 wait
+// states, tied to the registers so that every read stays behind it.
+__device__ __forceinline__ void mfma_result_fence(f32x4& x, f32x4& y) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(x), "+v"(y));
+}
+
+// Two floats to packed bf16, round-to-nearest-even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
-  // round-to-nearest-even to bf16 (finite values)
-  uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-  ua = (ua + 0x7fffu + ((ua >> 16) & 1u)) >> 16;
-  ub = (ub + 0x7fffu + ((ub >> 16) & 1u)) >> 16;
-  return ua | (ub << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
 template <int I, int N, typename F>
-__device__ __forceinline__ void attn_static_for(F& f) {
+__device__ __forceinline__ void attn_static_for(F&& f) {
   if constexpr (I < N) {
     f(std::integral_constant<int, I>{});
     attn_static_for<I + 1, N>(f);
@@ -169,8 +178,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   __shared__ __attribute__((aligned(16))) char p_lds[2][kAttnWaves * 64 * 16];  // P^T B-fragments per head block
   __shared__ float alpha_lds[2][64];
   __shared__ float scale_lds[64];
-  __shared__ __attribute__((aligned(16))) int valid_lds[kAttnRing][kAttnTK];  // 1 = key used
-  __shared__ int64_t rowoff_lds[kAttnRing][kAttnTK];     // byte offset of the key's KV row
+  __shared__ __attribute__((aligned(16))) float bias_lds[kAttnRing][kAttnTK];  // 0: key used, -inf: masked
+  __shared__ uint32_t rowoff_lds[kAttnRing][kAttnTK];    // offset of the key's KV row, 16-byte units
   __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[kAttnRing][2 * kAttnTK];  // raw index words
 
   const int lane = threadIdx.x & 63;
@@ -185,7 +194,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   const int hbase = hg * 64;
   const int hq = hbase + wave * 16 + i16;  // this lane's head in S^T
   const bool hvalid = hq < a.H;
-  const int ntiles = (a.K + kAttnTK - 1) / kAttnTK;
+  // with no KV rows every key is masked: the loop is skipped
+  const int ntiles = a.N > 0 ? (a.K + kAttnTK - 1) / kAttnTK : 0;
 
   const char* idx_row = static_cast<const char*>(a.idx) +
                         (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
@@ -212,44 +222,54 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
                                 : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[slot][lane]));
       const int j = t * kAttnTK + lane;
       const bool ok = j < a.K && raw >= 0 && raw < a.N;
-      valid_lds[slot][lane] = ok;
-      rowoff_lds[slot][lane] = (ok ? raw : 0) * a.kvsn * 2;
+      bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
+      rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
     }
   };
   // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
-  // holds chunk (e % CPR) ^ f(key) of key e / CPR.  Needs N > 0.  This
-  // thread's (key, chunk byte offset) per copy are fixed, computed once.
+  // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
+  // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
+  // source is kv + 16 (rowoff16[key] + dcoff).
   int dkey[SH::LPT], dcoff[SH::LPT];
 #pragma unroll
   for (int i = 0; i < SH::LPT; ++i) {
     const int e = i * SH::NT + static_cast<int>(threadIdx.x);
     dkey[i] = e / SH::CPR;
-    dcoff[i] = ((e % SH::CPR) ^ kv_swz<D>(dkey[i])) * 16;
+    dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
   }
-  auto issue_tile = [&](int t) {
+  uint32_t roff[SH::LPT];
+  auto read_roff = [&](int t) {
     const int slot = t % kAttnRing;
-    char* dst = kv_lds + slot * SH::TILE;
-    // all row offsets first, so the copies are not serialised behind LDS reads
-    int64_t roff[SH::LPT];
 #pragma unroll
-    for (int i = 0; i < SH::LPT; ++i) roff[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] : 0;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < SH::LPT; ++i) {
-      const int e0 = i * SH::NT + wave * 64;
-      if (e0 < SH::CH) {
-        // (passed as uint16_t*: a char* argument to this builtin makes clang
-        // drop the host launch stubs of later instantiations)
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + roff[i] + dcoff[i]);
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst + e0 * 16), 16, 0, 0);
-      }
+    for (int i = 0; i < SH::LPT; ++i)
+      roff[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+  };
+  // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
+  // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
+  auto dma = [&](int t, auto IC) {
+    constexpr int i = decltype(IC)::value;
+    const int e0 = i * SH::NT + wave * 64;
+    char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
+    // (passed as uint16_t*: a char* argument to this builtin makes clang
+    // drop the host launch stubs of later instantiations)
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+    if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+    } else if (e0 < SH::CH) {
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
     }
   };
+  auto issue_tile = [&](int t) {
+    read_roff(t);
+    attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
+  };
 
-  // Ring protocol: tile t lives in slot t % 3.  Iteration `it` consumes tile
-  // `it`; its one barrier (after the P^T exchange) is preceded by a full wait
-  // for the gather of tile it+1 and followed by the gather of tile it+2 into
-  // the slot of tile it-1, whose P.V every wave has finished by then.
+  // Ring protocol: tile t lives in slot t % 3 and its P^T in p_lds[t % 2].
+  // Iteration `it` computes P.V of tile `it` and S^T + softmax of tile it+1,
+  // and ends with the one barrier of the tile.  Before that barrier every
+  // wave waits for its copies of tile it+2 (issued at the start of the
+  // iteration, into the slot of tile it-1, which all waves finished in
+  // iteration it-1) and wave 0 publishes the indices of tile it+3.
 
   // ---- prologue: Q^T fragments, indices of tiles 0..2, gathers of tiles 0..1 ----
   bf16x8 qf[KS];
@@ -258,24 +278,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
   }
-  const bool has_kv = a.N > 0;
-  if (wave == 0 && ntiles > 0) {
-    load_idx(0);
-    if (ntiles > 1) load_idx(1);
-    if (ntiles > 2) load_idx(2);
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);
-    store_idx(0);
-    if (ntiles > 1) store_idx(1);
-  }
-  __syncthreads();
-  if (has_kv) {
-    if (ntiles > 0) issue_tile(0);
-    if (ntiles > 1) issue_tile(1);
-  }
-  // tile 0 landed; the gather of tile 1 may still be in flight
-  if (ntiles > 1 && has_kv) __builtin_amdgcn_s_waitcnt((SH::LPT & 0xF) | (0x7 << 4));
-  else __builtin_amdgcn_s_waitcnt(0x7 << 4);
-  __syncthreads();
+  const float sink_v = hvalid ? a.sink[hq] : 0.f;
 
   // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
   // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
@@ -299,16 +302,16 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
   float l_run = 0.f;       // this lane's share of the denominator
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int slot = it % kAttnRing;
-    const char* tile = kv_lds + slot * SH::TILE;
-
-    // ---- S^T = K Q^T for this wave's 16 heads: keys 16mb + 4g + r --------
-    // A-fragments stream through a QPD-deep register queue: each MFMA's
-    // operand was read from LDS QPD k-steps earlier.
-    constexpr int QPD = KS < 4 ? KS : 4;
-    const uint32_t qa_e = lds_addr(tile) + qbase + qadj;
-    const uint32_t qa_o = lds_addr(tile) + qbase - qadj;
+  // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
+  // A-fragments stream through a QPD-deep register queue: each MFMA's operand
+  // was read from LDS QPD k-steps earlier.  With ISSUE, the copies of tile
+  // t+1 are issued between the k-steps.
+  constexpr int QPD = KS < 4 ? KS : 4;
+  auto qk = [&](int t, f32x4 (&st)[2], auto ISSUE_C) {
+    constexpr bool ISSUE = decltype(ISSUE_C)::value;
+    const uint32_t tile = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE);
+    const uint32_t qa_e = tile + qbase + qadj;
+    const uint32_t qa_o = tile + qbase - qadj;
     bf16x8 kq[QPD][2];
     auto qk_issue = [&](auto KC) {
       constexpr int ks = decltype(KC)::value;
@@ -317,7 +320,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
       kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
     };
     attn_static_for<0, QPD>(qk_issue);
-    f32x4 st[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto qk_step = [&](auto KC) {
       constexpr int ks = decltype(KC)::value;
       constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
@@ -325,83 +329,84 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
       st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
       st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
       if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
+      if constexpr (ISSUE && ks % 2 == 0 && ks / 2 < SH::LPT) dma(t + 1, std::integral_constant<int, ks / 2>{});
     };
     attn_static_for<0, KS>(qk_step);
+    if constexpr (ISSUE && (KS + 1) / 2 < SH::LPT)
+      attn_static_for<(KS + 1) / 2, SH::LPT>([&](auto IC) { dma(t + 1, IC); });
+    mfma_result_fence(st[0], st[1]);
+  };
 
-    // ---- online softmax for head hq ---------------------------------------
-    const int4 v0 = *reinterpret_cast<const int4*>(&valid_lds[slot][4 * g]);
-    const int4 v1 = *reinterpret_cast<const int4*>(&valid_lds[slot][16 + 4 * g]);
+  // Online softmax of tile t for head hq, in registers, as kSmStages steps
+  // of similar VALU length so that they can be interleaved with the MFMAs of
+  // the previous tile's P.V; the result (P^T as a bf16 B-fragment and the
+  // head's rescale factor) is published by softmax_store.
+  struct SoftmaxOut {
+    u32x4 w;
+    float alpha;
+  };
+  struct SmState {
     float x[2][4];
-    x[0][0] = v0.x ? st[0][0] * a.scale_log2 : -__builtin_inff();
-    x[0][1] = v0.y ? st[0][1] * a.scale_log2 : -__builtin_inff();
-    x[0][2] = v0.z ? st[0][2] * a.scale_log2 : -__builtin_inff();
-    x[0][3] = v0.w ? st[0][3] * a.scale_log2 : -__builtin_inff();
-    x[1][0] = v1.x ? st[1][0] * a.scale_log2 : -__builtin_inff();
-    x[1][1] = v1.y ? st[1][1] * a.scale_log2 : -__builtin_inff();
-    x[1][2] = v1.z ? st[1][2] * a.scale_log2 : -__builtin_inff();
-    x[1][3] = v1.w ? st[1][3] * a.scale_log2 : -__builtin_inff();
-    float tmax = -__builtin_inff();
+    float tmax;
+    f32x2 p[4];
+    SoftmaxOut out;
+  };
+  constexpr int kSmStages = 6;
+  auto sm_stage = [&](SmState& S, const f32x4 (&st)[2], const f32x4 (&bias)[2], auto SC) {
+    constexpr int k = decltype(SC)::value;
+    if constexpr (k == 0) {  // scaled scores, masked keys at -inf; tile maximum
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tmax = __builtin_fmaxf(tmax, x[mb][r]);
-    {  // max over the four lane groups (xor 16, xor 32) with permlane swaps
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-      tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-      const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
-      tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
-    }
-    // First valid key of the head: the accumulator and denominator are still
-    // zero, so the reference moves without a rescale (alpha = 1).
-    const bool first = m_ref == -1.0e30f;
-    const bool raise = first ? tmax > m_ref : tmax > m_ref + kLazyRescale;
-    const float m_new = raise ? tmax : m_ref;
-    const float alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
-    m_ref = m_new;
-    float p[2][4];
-    float psum = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[mb][r] = __builtin_amdgcn_exp2f(x[mb][r] - m_new);
-        psum += p[mb][r];
-      }
-    l_run = l_run * alpha + psum;
-    {
+        for (int r = 0; r < 4; ++r) S.x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
+      S.tmax = __builtin_fmaxf(
+          __builtin_fmaxf(__builtin_fmaxf(S.x[0][0], S.x[0][1]), __builtin_fmaxf(S.x[0][2], S.x[0][3])),
+          __builtin_fmaxf(__builtin_fmaxf(S.x[1][0], S.x[1][1]), __builtin_fmaxf(S.x[1][2], S.x[1][3])));
+    } else if constexpr (k == 1) {  // max over lane groups g ^ 1
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(S.tmax), __float_as_uint(S.tmax), false, false);
+      S.tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    } else if constexpr (k == 2) {  // max over lane groups g ^ 2; move the reference
+      const SwapPair r32 = permlane32_swap(__float_as_uint(S.tmax), __float_as_uint(S.tmax));
+      const float tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+      // First valid key of the head: the accumulator and denominator are
+      // still zero, so the reference moves without a rescale (alpha = 1).
+      const bool first = m_ref == -1.0e30f;
+      const bool raise = first ? tmax > m_ref : tmax > m_ref + kLazyRescale;
+      const float m_new = raise ? tmax : m_ref;
+      S.out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
+      m_ref = m_new;
+    } else if constexpr (k == 3 || k == 4) {
+      constexpr int mb = k - 3;
+      S.p[2 * mb] = f32x2{__builtin_amdgcn_exp2f(S.x[mb][0] - m_ref), __builtin_amdgcn_exp2f(S.x[mb][1] - m_ref)};
+      S.p[2 * mb + 1] = f32x2{__builtin_amdgcn_exp2f(S.x[mb][2] - m_ref), __builtin_amdgcn_exp2f(S.x[mb][3] - m_ref)};
+    } else if constexpr (k == 5) {
+      const float psum = ((S.p[0][0] + S.p[0][1]) + (S.p[1][0] + S.p[1][1])) +
+                         ((S.p[2][0] + S.p[2][1]) + (S.p[3][0] + S.p[3][1]));
+      l_run = l_run * S.out.alpha + psum;
       // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
-      u32x4 w;
-      w[0] = f32x2_to_bf16x2(p[0][0], p[0][1]);
-      w[1] = f32x2_to_bf16x2(p[0][2], p[0][3]);
-      w[2] = f32x2_to_bf16x2(p[1][0], p[1][1]);
-      w[3] = f32x2_to_bf16x2(p[1][2], p[1][3]);
-      *reinterpret_cast<u32x4*>(&p_lds[it & 1][(wave * 64 + lane) * 16]) = w;
-      if (g == 0) alpha_lds[it & 1][wave * 16 + i16] = alpha;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S.out.w[c] = f32x2_to_bf16x2(S.p[c][0], S.p[c][1]);
     }
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // gather of tile it+1, indices of tile it+2, LDS traffic done
-    // indices of tile it+2 (copied one iteration ago) are published with P^T
-    if (wave == 0 && it + 2 < ntiles) store_idx(it + 2);
-    __syncthreads();
-    if (has_kv && it + 2 < ntiles) issue_tile(it + 2);
-    if (wave == 0 && it + 3 < ntiles) load_idx(it + 3);
+  };
+  auto softmax = [&](const f32x4 (&st)[2], const f32x4 (&bias)[2]) {
+    SmState S;
+    attn_static_for<0, kSmStages>([&](auto SC) { sm_stage(S, st, bias, SC); });
+    return S.out;
+  };
+  auto softmax_store = [&](int t, const SoftmaxOut& r) {
+    *reinterpret_cast<u32x4*>(&p_lds[t & 1][(wave * 64 + lane) * 16]) = r.w;
+    if (g == 0) alpha_lds[t & 1][wave * 16 + i16] = r.alpha;
+  };
 
-    // ---- O^T += V^T P^T for this wave's 16-dim blocks, all 64 heads -------
-    float al[4];
+  // O^T += V^T P^T of tile t for this wave's 16-dim blocks, all 64 heads.
+  // mix(0) is called once the first operand reads are out and mix(j+1)
+  // after the MFMAs of the wave's j-th block (j < MBW), so that independent
+  // VALU work issues while the reads and MFMAs are in flight.
+  auto pv = [&](int t, auto&& mix) {
+    const uint32_t ta = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE) + tbase;
     bf16x8 pb[4];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      al[nb] = alpha_lds[it & 1][nb * 16 + i16];
-      pb[nb] = *reinterpret_cast<const bf16x8*>(&p_lds[it & 1][(nb * 64 + lane) * 16]);
-    }
-    const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
-                                                         al[3] != 1.0f) != 0;
-    if (__builtin_expect(any_rescale, 0)) {
-#pragma unroll
-      for (int j = 0; j < MBW; ++j)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
-    }
-    const uint32_t ta = lds_addr(tile) + tbase;
+    for (int nb = 0; nb < 4; ++nb) pb[nb] = *reinterpret_cast<const bf16x8*>(&p_lds[t & 1][(nb * 64 + lane) * 16]);
     if constexpr (SH::MBT % kAttnWaves == 0) {
       // every wave owns MBW blocks; the reads of blocks j+1 and j+2 are in
       // flight while block j's MFMAs run
@@ -412,6 +417,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
         lo[1] = tr_read<128>(ta);
         hi[1] = tr_read<16 * ROW + 128>(ta);
       }
+      __builtin_amdgcn_sched_barrier(0);  // operand reads go out before any mixed-in VALU
+      mix(std::integral_constant<int, 0>{});
       auto step = [&](auto JC) {
         constexpr int j = decltype(JC)::value;
         if constexpr (j + 2 < MBW) {
@@ -427,6 +434,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[j][nb], 0, 0, 0);
+        mix(std::integral_constant<int, j + 1>{});
       };
       attn_static_for<0, MBW>(step);
     } else {
@@ -440,7 +448,92 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
         for (int nb = 0; nb < 4; ++nb)
           oacc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[0][nb], 0, 0, 0);
       }
+      mix(std::integral_constant<int, 0>{});
+      mix(std::integral_constant<int, 1>{});
     }
+  };
+
+  // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r).
+  auto read_bias = [&](int t, f32x4 (&bias)[2]) {
+    bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
+    bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
+  };
+
+  // One iteration (see the ring protocol above).  ISSUE: tile it+2 exists;
+  // NEXT: tile it+1 exists.
+  auto iteration = [&](int it, auto ISSUE_C, auto NEXT_C) {
+    constexpr bool ISSUE = decltype(ISSUE_C)::value;
+    constexpr bool NEXT = decltype(NEXT_C)::value;
+    // LDS reads first: row offsets of tile it+2, key biases of tile it+1
+    if constexpr (ISSUE) read_roff(it + 2);
+    f32x4 bias[2];
+    if constexpr (NEXT) read_bias(it + 1, bias);
+    if (ISSUE && wave == 0 && it + 3 < ntiles) load_idx(it + 3);
+    f32x4 st[2];
+    if constexpr (NEXT) qk(it + 1, st, ISSUE_C);
+    // softmax stage 0 (scaled, masked scores and their maximum) frees the
+    // raw scores and biases before the branch; the rest is interleaved below
+    SmState S;
+    if constexpr (NEXT) sm_stage(S, st, bias, std::integral_constant<int, 0>{});
+    // rescale factors of tile it (read after S^T so that their wait does not
+    // stall the S^T operand queue)
+    float al[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+    const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
+                                                         al[3] != 1.0f) != 0;
+    if (__builtin_expect(any_rescale, 0)) {
+#pragma unroll
+      for (int j = 0; j < MBW; ++j)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
+    }
+    // P.V of tile it with the softmax of tile it+1 interleaved
+    auto mix = [&](auto KC) {
+      constexpr int k = decltype(KC)::value + 1;
+      if constexpr (NEXT && k < kSmStages) sm_stage(S, st, bias, std::integral_constant<int, k>{});
+    };
+    pv(it, mix);
+    if constexpr (NEXT) {
+      constexpr int done = (MBW + 2) < kSmStages ? (MBW + 2) : kSmStages;
+      attn_static_for<done, kSmStages>([&](auto SC) { sm_stage(S, st, bias, SC); });
+      softmax_store(it + 1, S.out);
+    }
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // copies of tile it+2 and indices of tile it+3 landed
+    if (ISSUE && wave == 0 && it + 3 < ntiles) store_idx(it + 3);
+    __syncthreads();
+  };
+
+  if (ntiles > 0) {
+    if (wave == 0) {
+      load_idx(0);
+      if (ntiles > 1) load_idx(1);
+      if (ntiles > 2) load_idx(2);
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);
+      store_idx(0);
+      if (ntiles > 1) store_idx(1);
+    }
+    __syncthreads();
+    issue_tile(0);
+    if (ntiles > 1) issue_tile(1);
+    // tile 0 landed; the copies of tile 1 may still be in flight
+    if (ntiles > 1) __builtin_amdgcn_s_waitcnt((SH::LPT & 0xF) | (0x7 << 4));
+    else __builtin_amdgcn_s_waitcnt(0x7 << 4);
+    __syncthreads();
+    {
+      f32x4 bias[2];
+      read_bias(0, bias);
+      f32x4 st[2];
+      qk(0, st, std::false_type{});
+      softmax_store(0, softmax(st, bias));
+    }
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // tile 1 landed
+    if (wave == 0 && ntiles > 2) store_idx(2);
+    __syncthreads();
+    int it = 0;
+    for (; it + 2 < ntiles; ++it) iteration(it, std::true_type{}, std::true_type{});
+    if (it + 1 < ntiles) iteration(it++, std::false_type{}, std::true_type{});
+    iteration(it, std::false_type{}, std::false_type{});
   }
 
   // ---- finish: denominators, sink, normalisation, lse ---------------------
@@ -452,7 +545,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
   }
   constexpr float kLog2e = 1.4426950408889634f;
-  const float sink2 = hvalid ? a.sink[hq] * kLog2e : -__builtin_inff();
+  const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
   const float m_fin = __builtin_fmaxf(m_ref, sink2);
   const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
   const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
@@ -535,6 +628,9 @@ extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kv)) & 15)
     return set_error(SI_ERR_INVALID, "q/kv must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(o) & 15) return set_error(SI_ERR_INVALID, "o must be 16-byte aligned");
+  // KV row offsets are kept in 32 bits, in 16-byte units, inside one batch.
+  if (N_kv > 0 && ((N_kv - 1) * kv_strides[1] + D) / 8 >= (int64_t{1} << 32))
+    return set_error(SI_ERR_UNSUPPORTED, "kv batch larger than 64 GiB");
   SparseAttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
