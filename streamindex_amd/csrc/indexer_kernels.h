@@ -270,8 +270,14 @@ void indexer_topk_kernel(IndexerArgs a) {
   constexpr int RING = TopkShape<C>::RING;
   // The DMA-filled K ring sits first (global_load_lds destinations stay
   // below 64 KiB), then the per-wave selection buffers.
-  __shared__ __attribute__((aligned(16))) char lds[RING * TILE_BYTES + NW * C * 8];
+  // Compaction requests of the waves (double-buffered by tile parity) are
+  // posted before each tile barrier, where LDS has room for them.
+  constexpr int SEL_END = RING * TILE_BYTES + NW * C * 8;
+  constexpr bool SHARE_COMP = SEL_END + 2 * NW * 4 <= 160 * 1024;
+  __shared__ __attribute__((aligned(16))) char lds[SEL_END + (SHARE_COMP ? 2 * NW * 4 : 0)];
   uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + RING * TILE_BYTES);
+  int* const comp_req = reinterpret_cast<int*>(lds + SEL_END);
+  static_assert(NW == 4, "the requests of a tile are read as one int4");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -358,7 +364,13 @@ void indexer_topk_kernel(IndexerArgs a) {
     // finished before the barrier that ended the previous iteration.
     const int fill = slot == 0 ? RING - 1 : slot - 1;
     const bool more = it + RING - 1 < ntiles;
+    int4 rq = int4{0, 0, 0, 0};
+    if (SHARE_COMP && it > 0) rq = *reinterpret_cast<const int4*>(comp_req + ((it - 1) & 1) * NW);
     if (more) ld.issue(kb, a.kst, (it + RING - 1) * TILE_N, a.T, lds + fill * TILE_BYTES);
+    // A compaction that some row asked for at the previous barrier runs now
+    // in every row that is close to needing one, so that the workgroup waits
+    // once for all of them instead of once per row.
+    if (SHARE_COMP && (rq.x | rq.y | rq.z | rq.w) && sel.wants_compaction()) sel.compact(lane);
     const char* tile = lds + slot * TILE_BYTES;
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
@@ -425,13 +437,21 @@ void indexer_topk_kernel(IndexerArgs a) {
         offer_tile(p0, 0.f, tbase, true, cur_mask);
       }
     }
-    if (sel.needs_compaction()) sel.compact(lane);
+    // Every offer needs room for 64 keys and a tile makes at most two
+    // (a partial tile drains the pending one first): a row holding more than
+    // C - 128 keys compacts before its next offer.
+    if constexpr (SHARE_COMP) {
+      comp_req[(it & 1) * NW + wave] = sel.needs_compaction();
+    } else {
+      if (sel.needs_compaction()) sel.compact(lane);
+    }
     // Tile it+1 must have landed; the copies of tile it+RING-1 may stay in flight.
     if (RING == 3 && more) wait_vm_lgkm0<LPT>(); else wait_vm_lgkm0<0>();
     __syncthreads();
     slot = slot == RING - 1 ? 0 : slot + 1;
   }
 
+  if (sel.needs_compaction()) sel.compact(lane);  // room for the pending offer
   if (pend) drain();
 
   if (active) {

@@ -146,19 +146,30 @@ struct WaveSelect {
   // Compacting whenever more than C - 128 keys are held leaves room for two
   // 64-key offers before the next check.
   __device__ __forceinline__ bool needs_compaction() const { return n > C - 2 * kWave; }
+  // Most keys compact() keeps.
+  __device__ __forceinline__ int compact_cmax() const { return top_k + kWave < CMAX ? top_k + kWave : CMAX; }
+  // Close enough to needing a compaction that joining one that another row
+  // of the workgroup needs is worthwhile: more than halfway from what a
+  // compaction keeps to the compaction threshold.
+  __device__ __forceinline__ bool wants_compaction() const { return n > (compact_cmax() + C - 2 * kWave) / 2; }
 
+  // Bits of a per-lane count in [0, E].
+  static constexpr int EBITS = E < 16 ? 4 : (E < 32 ? 5 : (E < 64 ? 6 : 7));
+
+  // Keys counted per lane in VALU, then summed over the wave with one ballot
+  // per count bit.
   __device__ __forceinline__ static int count_hi_ge(const uint64_t (&v)[E], uint32_t h) {
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) c += __builtin_popcountll(ballot64(key_hi(v[j]) >= h));
-    return c;
+    for (int j = 0; j < E; ++j) c += key_hi(v[j]) >= h ? 1 : 0;
+    return wave_count_sum<EBITS>(c);
   }
 
   __device__ __forceinline__ static int count_ge(const uint64_t (&v)[E], uint64_t p) {
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) c += __builtin_popcountll(ballot64(v[j] >= p));
-    return c;
+    for (int j = 0; j < E; ++j) c += v[j] >= p ? 1 : 0;
+    return wave_count_sum<EBITS>(c);
   }
 
   // Raises the floor so that kk <= n <= cmax (needs n > cmax and kk <= cmax).
@@ -169,13 +180,12 @@ struct WaveSelect {
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       const int pos = j * kWave + lane;
-      v[j] = pos < n ? buf[pos] : 0ull;  // empty slots hold key 0: never counted (every probe is >= 1)
+      const uint64_t x = buf[pos];
+      v[j] = pos < n ? x : 0ull;
       mx = key_hi(v[j]) > mx ? key_hi(v[j]) : mx;
     }
     mx = wave_max_u32(mx);
     const int target = kk + (cmax - kk) / 4;
-
-    // Invariant: count(hi >= lo) = c_lo > cmax and count(hi >= hi_) = c_hi < kk.
     uint64_t lo = tau, hi_ = static_cast<uint64_t>(mx) + 1;
     int c_lo = n, c_hi = 0;
     uint64_t P = 0;
@@ -187,8 +197,9 @@ struct WaveSelect {
       if (it & 1) {
         step = span >> 1;
       } else {
-        const float f = static_cast<float>(c_lo - target) / static_cast<float>(c_lo - c_hi);
-        step = static_cast<uint64_t>(static_cast<float>(span) * f);
+        const float f = static_cast<float>(c_lo - target) * __builtin_amdgcn_rcpf(static_cast<float>(c_lo - c_hi));
+        const float half_span = static_cast<float>(static_cast<uint32_t>(span >> 1));
+        step = static_cast<uint64_t>(static_cast<uint32_t>(half_span * __builtin_fminf(f, 1.0f))) << 1;
       }
       step = step < 1 ? 1 : (step > span - 1 ? span - 1 : step);
       const uint32_t mid = static_cast<uint32_t>(lo + step);
@@ -207,7 +218,6 @@ struct WaveSelect {
       }
     }
     if (!found) {
-      // Many keys share the ordered score `lo`: bisect over the full key.
       uint64_t plo = lo << 32;
       uint64_t phi = hi_ >= (1ull << 32) ? ~0ull : (hi_ << 32);
       for (int it = 0; it < 64 && phi - plo > 1; ++it) {
@@ -220,22 +230,23 @@ struct WaveSelect {
         }
         if (c > cmax) plo = mid; else phi = mid;
       }
-      if (!found) {  // unreachable for distinct keys; keep the capacity bound
+      if (!found) {
         P = phi;
         c = count_ge(v, P);
       }
     }
-    // Dense write-back: survivors to [0, c), the rest past c (never read).
-    // Every key is already in registers, so the in-place writes are safe.
-    int base = 0;
+    wave_lds_sync();
+    int keep_l = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) keep_l += v[j] >= P ? 1 : 0;
+    const int kbase = wave_incl_scan(keep_l, lane) - keep_l;
+    const int dbase = c + lane * E - kbase;
+    int kept = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       const bool keep = v[j] >= P;
-      const uint64_t bal = ballot64(keep);
-      const int below = lanes_below(bal);
-      const int pos = keep ? base + below : c + (j * kWave + lane - base - below);
-      buf[pos] = v[j];
-      base += __builtin_popcountll(bal);
+      buf[keep ? kbase + kept : dbase + (j - kept)] = v[j];
+      kept += keep ? 1 : 0;
     }
     n = __builtin_amdgcn_readfirstlane(c);
     floor_key = P;
@@ -244,9 +255,7 @@ struct WaveSelect {
   }
 
   // Keeping close to top_k keys leaves the most room and the highest floor.
-  __device__ __forceinline__ void compact(int lane) {
-    compact_to(lane, top_k, top_k + 64 < CMAX ? top_k + 64 : CMAX);
-  }
+  __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, compact_cmax()); }
 
   // Sorted top_k of the row: indices (int64, -1 pad) and scores (fp32, -inf pad).
   // When top_k fits in half the buffer, the held keys are first cut to at
