@@ -61,7 +61,7 @@ struct SparseAttnArgs {
 
 constexpr int kAttnTK = 32;      // keys per tile
 constexpr int kAttnWaves = 4;    // waves per workgroup; 16 heads each in S^T
-constexpr int kAttnRing = 3;     // KV tiles resident in LDS
+constexpr int kAttnRing = 4;     // KV tiles resident in LDS
 // The reference maximum of a head moves only when a tile's maximum exceeds it
 // by 2^64 (log2 units): p = 2^(x - m_ref) then stays below 2^64, far inside
 // the fp32/bf16 exponent range, and the output accumulator is rescaled only
@@ -168,6 +168,62 @@ __device__ __forceinline__ void attn_static_for(F&& f) {
   }
 }
 
+// s_waitcnt immediate: vmcnt <= n (6-bit field: bits 3:0 and 15:14),
+// lgkmcnt = 0, expcnt not waited (gfx9 encoding).
+constexpr int vm_lgkm0(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4); }
+
+// Waits until at most N LDS operations of this wave are outstanding (no
+// registers tied; follow with reg_tie on the registers the wait covers).
+template <int N>
+__device__ __forceinline__ void lds_wait_n() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
+// Keeps every use of x after the preceding inline-asm wait.
+template <typename T>
+__device__ __forceinline__ void reg_tie(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// Issue order of the pipelined LDS reads of one tile iteration (all from
+// inline asm, so the wait counts are exact).  Step u (u < 4 MBW) runs the
+// P.V MFMA of V^T block u/4 and head block u%4 and, for u < KS with QK, the
+// two S^T MFMAs of k-step u.  Issued first: 4 P^T fragments, V^T blocks 0
+// and 1 (two reads each), the S^T operands of k-steps 0..QPD-1 (two reads
+// each); after the MFMAs of step u: the S^T operands of k-step u + QPD and,
+// when u % 4 == 0, V^T block u/4 + 2.
+template <int KS, int MBW, bool QK>
+struct AttnSched {
+  static constexpr int QPD = KS < 4 ? KS : 4;
+  static constexpr int NSTEP = 4 * MBW;  // >= KS for every supported D
+  static constexpr int PRE_TR = MBW > 1 ? 4 : 2;
+  static constexpr int PRE = 4 + PRE_TR + (QK ? 2 * QPD : 0);
+  static constexpr bool kq_at(int u) { return QK && u + QPD < KS; }
+  static constexpr bool tr_at(int u) { return u % 4 == 0 && u / 4 + 2 < MBW; }
+  static constexpr int issued_before(int u) {
+    int n = PRE;
+    for (int i = 0; i < u; ++i) n += (kq_at(i) ? 2 : 0) + (tr_at(i) ? 2 : 0);
+    return n;
+  }
+  // issue index of the second read of S^T k-step k / of V^T block j
+  static constexpr int kq_last(int k) { return k < QPD ? 4 + PRE_TR + 2 * k + 1 : issued_before(k - QPD) + 1; }
+  static constexpr int tr_last(int j) {
+    return j < 2 ? 4 + 2 * j + 1 : issued_before(4 * (j - 2)) + (kq_at(4 * (j - 2)) ? 2 : 0) + 1;
+  }
+  // LDS reads that may stay outstanding before step u's MFMAs (-1: no wait)
+  static constexpr int wait_at(int u) {
+    int need = -1;
+    if (QK && u < KS && kq_last(u) > need) need = kq_last(u);
+    if (u % 4 == 0 && tr_last(u / 4) > need) need = tr_last(u / 4);
+    if (u == 0 && need < 3) need = 3;  // the P^T fragments
+    if (need < 0) return -1;
+    const int w = issued_before(u) - 1 - need;
+    return w < 15 ? w : 15;  // lgkmcnt field limit (a lower count only waits longer)
+  }
+  // step at which softmax stage k (of NSM) runs: spread over the steps that
+  // follow the last S^T MFMA
+  static constexpr int sm_step(int k, int NSM) { return KS + k * (NSTEP - KS) / NSM; }
+};
+
 template <int D, bool IDX64>
 __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
   using SH = AttnShape<D>;
@@ -180,7 +236,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   __shared__ float scale_lds[64];
   __shared__ __attribute__((aligned(16))) float bias_lds[kAttnRing][kAttnTK];  // 0: key used, -inf: masked
   __shared__ uint32_t rowoff_lds[kAttnRing][kAttnTK];    // offset of the key's KV row, 16-byte units
-  __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[kAttnRing][2 * kAttnTK];  // raw index words
+  __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[2 * kAttnRing][2 * kAttnTK];  // raw index words
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -202,7 +258,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
 
   // Key indices of tile `t`: wave 0 copies the raw index words into
-  // idxraw_lds[t % 3] with a global_load_lds (nothing lands in registers, so
+  // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
   // no loop-carried load result forces an early wait), and after its next
   // full wait reads them back, validates them and publishes validity and row
   // byte offsets to ring slot t % 3 for every wave.
@@ -212,14 +268,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
     const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
-                                     (lds_void_t*)(&idxraw_lds[t % kAttnRing][0]), 4, 0, 0);
+                                     (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
   };
   auto store_idx = [&](int t) {
     const int slot = t % kAttnRing;
+    const int rslot = t % (2 * kAttnRing);
     if (lane < kAttnTK) {
-      const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[slot][2 * lane + 1]) << 32) |
-                                                       idxraw_lds[slot][2 * lane])
-                                : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[slot][lane]));
+      const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
+                                                       idxraw_lds[rslot][2 * lane])
+                                : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
       const int j = t * kAttnTK + lane;
       const bool ok = j < a.K && raw >= 0 && raw < a.N;
       bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
@@ -237,12 +294,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     dkey[i] = e / SH::CPR;
     dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
   }
-  uint32_t roff[SH::LPT];
-  auto read_roff = [&](int t) {
+  uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
+  auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
     const int slot = t % kAttnRing;
 #pragma unroll
     for (int i = 0; i < SH::LPT; ++i)
-      roff[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+      dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
   };
   // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
   // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
@@ -260,18 +317,22 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     }
   };
   auto issue_tile = [&](int t) {
-    read_roff(t);
+    read_roff(t, roff);
     attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
   };
 
-  // Ring protocol: tile t lives in slot t % 3 and its P^T in p_lds[t % 2].
-  // Iteration `it` computes P.V of tile `it` and S^T + softmax of tile it+1,
-  // and ends with the one barrier of the tile.  Before that barrier every
-  // wave waits for its copies of tile it+2 (issued at the start of the
-  // iteration, into the slot of tile it-1, which all waves finished in
-  // iteration it-1) and wave 0 publishes the indices of tile it+3.
+  // Ring protocol: tile t lives in slot t % 4 and its P^T in p_lds[t % 2].
+  // Iteration `it` computes P.V of tile it and S^T + softmax of tile it+1,
+  // and ends with the one barrier of the tile.  The copies of tile it+3 are
+  // issued from the start of the iteration into the slot of tile it-1 (which
+  // all waves finished in iteration it-1) and must land by the end of
+  // iteration it+1: two iterations of gather latency.  Wave 0 copies the raw
+  // indices of tile it+6 at the start and publishes those of tile it+5
+  // (copied one iteration earlier) before the barrier; the row offsets of tile it+4 and
+  // the key biases of tile it+2 are read one iteration ahead into registers,
+  // so an iteration starts its copies and its softmax without waiting for LDS.
 
-  // ---- prologue: Q^T fragments, indices of tiles 0..2, gathers of tiles 0..1 ----
+  // ---- Q^T fragments and the sink --------------------------------------------
   bf16x8 qf[KS];
   {
     const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
@@ -398,88 +459,35 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
     if (g == 0) alpha_lds[t & 1][wave * 16 + i16] = r.alpha;
   };
 
-  // O^T += V^T P^T of tile t for this wave's 16-dim blocks, all 64 heads.
-  // mix(0) is called once the first operand reads are out and mix(j+1)
-  // after the MFMAs of the wave's j-th block (j < MBW), so that independent
-  // VALU work issues while the reads and MFMAs are in flight.
-  auto pv = [&](int t, auto&& mix) {
-    const uint32_t ta = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE) + tbase;
-    bf16x8 pb[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) pb[nb] = *reinterpret_cast<const bf16x8*>(&p_lds[t & 1][(nb * 64 + lane) * 16]);
-    if constexpr (SH::MBT % kAttnWaves == 0) {
-      // every wave owns MBW blocks; the reads of blocks j+1 and j+2 are in
-      // flight while block j's MFMAs run
-      v4i16 lo[3], hi[3];
-      lo[0] = tr_read<0>(ta);
-      hi[0] = tr_read<16 * ROW>(ta);
-      if constexpr (MBW > 1) {
-        lo[1] = tr_read<128>(ta);
-        hi[1] = tr_read<16 * ROW + 128>(ta);
-      }
-      __builtin_amdgcn_sched_barrier(0);  // operand reads go out before any mixed-in VALU
-      mix(std::integral_constant<int, 0>{});
-      auto step = [&](auto JC) {
-        constexpr int j = decltype(JC)::value;
-        if constexpr (j + 2 < MBW) {
-          lo[(j + 2) % 3] = tr_read<128 * (j + 2)>(ta);
-          hi[(j + 2) % 3] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
-          lds_wait<4>(lo[j % 3], hi[j % 3]);
-        } else if constexpr (j + 1 < MBW) {
-          lds_wait<2>(lo[j % 3], hi[j % 3]);
-        } else {
-          lds_wait<0>(lo[j % 3], hi[j % 3]);
-        }
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j % 3], hi[j % 3], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[j][nb], 0, 0, 0);
-        mix(std::integral_constant<int, j + 1>{});
-      };
-      attn_static_for<0, MBW>(step);
-    } else {
-      // fewer 16-dim blocks than waves (D = 32): waves past the last block idle
-      if (wave < SH::MBT) {
-        v4i16 lo = tr_read<0>(ta);
-        v4i16 hi = tr_read<16 * ROW>(ta);
-        lds_wait<0>(lo, hi);
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          oacc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[nb], oacc[0][nb], 0, 0, 0);
-      }
-      mix(std::integral_constant<int, 0>{});
-      mix(std::integral_constant<int, 1>{});
-    }
-  };
-
   // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r).
   auto read_bias = [&](int t, f32x4 (&bias)[2]) {
     bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
     bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
   };
 
-  // One iteration (see the ring protocol above).  ISSUE: tile it+2 exists;
-  // NEXT: tile it+1 exists.
-  auto iteration = [&](int it, auto ISSUE_C, auto NEXT_C) {
+  // One pipelined iteration.  P.V of tile it (O^T += V^T P^T for this wave's
+  // 16-dim blocks, all 64 heads) runs alongside S^T of tile it+1 and then
+  // alongside the softmax of tile it+1, in one stream of MFMAs; the copies
+  // of tile it+3 are issued in between.  ISSUE: tile it+3 exists; NXT: tile
+  // it+1 exists; WAIT2: tile it+2 exists (its copies must land by the end).
+  f32x4 bias_cur[2], bias_nx[2];   // key biases of tiles it+1 and it+2
+  uint32_t roff_nx[SH::LPT];       // copy sources of tile it+4
+  constexpr int kPreCopies = SH::LPT < 3 ? SH::LPT : 3;  // copies issued before the MFMA stream
+  auto iteration = [&](int it, auto ISSUE_C, auto NXT_C, auto WAIT2_C) {
     constexpr bool ISSUE = decltype(ISSUE_C)::value;
-    constexpr bool NEXT = decltype(NEXT_C)::value;
-    // LDS reads first: row offsets of tile it+2, key biases of tile it+1
-    if constexpr (ISSUE) read_roff(it + 2);
-    f32x4 bias[2];
-    if constexpr (NEXT) read_bias(it + 1, bias);
-    if (ISSUE && wave == 0 && it + 3 < ntiles) load_idx(it + 3);
-    f32x4 st[2];
-    if constexpr (NEXT) qk(it + 1, st, ISSUE_C);
-    // softmax stage 0 (scaled, masked scores and their maximum) frees the
-    // raw scores and biases before the branch; the rest is interleaved below
-    SmState S;
-    if constexpr (NEXT) sm_stage(S, st, bias, std::integral_constant<int, 0>{});
-    // rescale factors of tile it (read after S^T so that their wait does not
-    // stall the S^T operand queue)
+    constexpr bool NXT = decltype(NXT_C)::value;
+    constexpr bool WAIT2 = decltype(WAIT2_C)::value;
+    using SC = AttnSched<KS, MBW, NXT>;
+    // ---- rescale factors of tile it (needed now); row offsets of tile it+4
+    // and key biases of tile it+2 (for the next iteration; the slots read are
+    // always inside the arrays, so the reads need no guard)
     float al[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+    read_roff(it + 4, roff_nx);
+    read_bias(it + 2, bias_nx);
+    if (wave == 0 && it + 6 < ntiles) load_idx(it + 6);
+    if constexpr (ISSUE) attn_static_for<0, kPreCopies>([&](auto IC) { dma(it + 3, IC); });
     const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
                                                          al[3] != 1.0f) != 0;
     if (__builtin_expect(any_rescale, 0)) {
@@ -488,37 +496,116 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
     }
-    // P.V of tile it with the softmax of tile it+1 interleaved
-    auto mix = [&](auto KC) {
-      constexpr int k = decltype(KC)::value + 1;
-      if constexpr (NEXT && k < kSmStages) sm_stage(S, st, bias, std::integral_constant<int, k>{});
-    };
-    pv(it, mix);
-    if constexpr (NEXT) {
-      constexpr int done = (MBW + 2) < kSmStages ? (MBW + 2) : kSmStages;
-      attn_static_for<done, kSmStages>([&](auto SC) { sm_stage(S, st, bias, SC); });
-      softmax_store(it + 1, S.out);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- pipelined LDS reads, in the order AttnSched describes
+    const uint32_t pa = lds_addr(&p_lds[it & 1][0]) + lane * 16;
+    bf16x8 pbr[4];
+    pbr[0] = ld128<0>(pa);
+    pbr[1] = ld128<1024>(pa);
+    pbr[2] = ld128<2048>(pa);
+    pbr[3] = ld128<3072>(pa);
+    const uint32_t ta = lds_addr(kv_lds + (it % kAttnRing) * SH::TILE) + tbase;
+    v4i16 lo[3], hi[3];
+    lo[0] = tr_read<0>(ta);
+    hi[0] = tr_read<16 * ROW>(ta);
+    if constexpr (MBW > 1) {
+      lo[1] = tr_read<128>(ta);
+      hi[1] = tr_read<16 * ROW + 128>(ta);
     }
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // copies of tile it+2 and indices of tile it+3 landed
-    if (ISSUE && wave == 0 && it + 3 < ntiles) store_idx(it + 3);
+    const uint32_t qtile = lds_addr(kv_lds + ((it + 1) % kAttnRing) * SH::TILE);
+    const uint32_t qa_e = qtile + qbase + qadj;
+    const uint32_t qa_o = qtile + qbase - qadj;
+    constexpr int QPD = SC::QPD;
+    bf16x8 kq[QPD][2];
+    auto kq_issue = [&](auto KC) {
+      constexpr int ks = decltype(KC)::value;
+      const uint32_t base = (ks & 1) ? qa_o : qa_e;
+      kq[ks % QPD][0] = ld128<64 * ks>(base);
+      kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+    };
+    if constexpr (NXT) attn_static_for<0, QPD>(kq_issue);
+
+    f32x4 st[2];
+    SmState S;
+    auto step = [&](auto UC) {
+      constexpr int u = decltype(UC)::value;
+      constexpr int w = SC::wait_at(u);
+      if constexpr (w >= 0) lds_wait_n<w>();
+      if constexpr (NXT && u < KS) {
+        reg_tie(kq[u % QPD][0]);
+        reg_tie(kq[u % QPD][1]);
+      }
+      if constexpr (u % 4 == 0) {
+        reg_tie(lo[(u / 4) % 3]);
+        reg_tie(hi[(u / 4) % 3]);
+      }
+      if constexpr (u == 0) {
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) reg_tie(pbr[nb]);
+      }
+      if constexpr (NXT && u < KS) {
+        const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+        st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[u % QPD][0], qf[u], u == 0 ? z : st[0], 0, 0, 0);
+        st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[u % QPD][1], qf[u], u == 0 ? z : st[1], 0, 0, 0);
+      }
+      {
+        constexpr int j = u / 4, nb = u % 4;
+        const bf16x8 vf =
+            __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j % 3], hi[j % 3], 0, 1, 2, 3, 4, 5, 6, 7));
+        oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pbr[nb], oacc[j][nb], 0, 0, 0);
+      }
+      if constexpr (SC::kq_at(u)) kq_issue(std::integral_constant<int, u + QPD>{});
+      if constexpr (SC::tr_at(u)) {
+        constexpr int j2 = u / 4 + 2;
+        lo[j2 % 3] = tr_read<128 * j2>(ta);
+        hi[j2 % 3] = tr_read<16 * ROW + 128 * j2>(ta);
+      }
+      if constexpr (ISSUE && u + kPreCopies < SH::LPT) dma(it + 3, std::integral_constant<int, u + kPreCopies>{});
+      if constexpr (NXT) {
+        attn_static_for<0, kSmStages>([&](auto KC) {
+          constexpr int k = decltype(KC)::value;
+          if constexpr (SC::sm_step(k, kSmStages) == u) sm_stage(S, st, bias_cur, KC);
+        });
+      }
+    };
+    attn_static_for<0, SC::NSTEP>(step);
+    if constexpr (NXT) softmax_store(it + 1, S.out);
+    bias_cur[0] = bias_nx[0];
+    bias_cur[1] = bias_nx[1];
+#pragma unroll
+    for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
+    // copies of tile it+2 and indices of tile it+5 (both issued one iteration
+    // ago) landed; the copies of tile it+3 and, in wave 0, the indices of
+    // tile it+6 may stay in flight
+    if constexpr (WAIT2 && ISSUE) {
+      if (wave == 0 && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT + 1));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+    }
+    if (wave == 0 && it + 5 < ntiles) store_idx(it + 5);
     __syncthreads();
   };
 
   if (ntiles > 0) {
+    // indices of tiles 0..5; tile 4 shares its row-offset / bias slot with
+    // tile 0, so it is published once tile 0's entries have been read, and
+    // tile 5 at the end of iteration 0
     if (wave == 0) {
-      load_idx(0);
-      if (ntiles > 1) load_idx(1);
-      if (ntiles > 2) load_idx(2);
+      const int np = ntiles < 6 ? ntiles : 6;
+      for (int t = 0; t < np; ++t) load_idx(t);
       __builtin_amdgcn_s_waitcnt(0x7 << 4);
-      store_idx(0);
-      if (ntiles > 1) store_idx(1);
+      for (int t = 0; t < np && t < 4; ++t) store_idx(t);
     }
     __syncthreads();
     issue_tile(0);
     if (ntiles > 1) issue_tile(1);
-    // tile 0 landed; the copies of tile 1 may still be in flight
-    if (ntiles > 1) __builtin_amdgcn_s_waitcnt((SH::LPT & 0xF) | (0x7 << 4));
-    else __builtin_amdgcn_s_waitcnt(0x7 << 4);
+    if (ntiles > 2) issue_tile(2);
+    // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
+    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
     __syncthreads();
     {
       f32x4 bias[2];
@@ -527,13 +614,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
       qk(0, st, std::false_type{});
       softmax_store(0, softmax(st, bias));
     }
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // tile 1 landed
-    if (wave == 0 && ntiles > 2) store_idx(2);
+    read_bias(1, bias_cur);
+    read_roff(3, roff);
+    // tile 1 landed; the copies of tile 2 may still be in flight
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+    else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+    __syncthreads();  // also: every wave has read tile 0's row offsets and biases
+    if (wave == 0 && ntiles > 4) store_idx(4);
     __syncthreads();
     int it = 0;
-    for (; it + 2 < ntiles; ++it) iteration(it, std::true_type{}, std::true_type{});
-    if (it + 1 < ntiles) iteration(it++, std::false_type{}, std::true_type{});
-    iteration(it, std::false_type{}, std::false_type{});
+    for (; it + 3 < ntiles; ++it) iteration(it, std::true_type{}, std::true_type{}, std::true_type{});
+    if (it + 2 < ntiles) iteration(it++, std::false_type{}, std::true_type{}, std::true_type{});
+    if (it + 1 < ntiles) iteration(it++, std::false_type{}, std::true_type{}, std::false_type{});
+    iteration(it, std::false_type{}, std::false_type{}, std::false_type{});
   }
 
   // ---- finish: denominators, sink, normalisation, lse ---------------------

@@ -104,6 +104,22 @@ def test_head_dims(cuda_device, D):
     _check(q, kv, sink, idx, D ** -0.5, o, lse, f"D={D}")
 
 
+@pytest.mark.parametrize("D,K,i64", [(576, 160, False), (576, 256, True), (576, 512, False), (128, 192, True),
+                                     (64, 256, False), (256, 224, False)])
+def test_tile_pipeline_depths(cuda_device, D, K, i64):
+    # 5..16 key tiles: the steady-state iteration, its three tail variants and
+    # the index prefetch distance all run (up to 4 tiles only the tails run)
+    B, S, H, N = 1, 16, 64, 512
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=500 + K, q_scale=0.5, kv_scale=0.5)
+    g = torch.Generator().manual_seed(K)
+    idx = torch.randint(0, N, (B, S, K), generator=g, dtype=torch.int64 if i64 else torch.int32)
+    idx[:, :, ::5] = -1
+    idx = idx.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, D ** -0.5)
+    torch.cuda.synchronize()
+    _check(q, kv, sink, idx, D ** -0.5, o, lse, f"D={D} K={K}")
+
+
 @pytest.mark.parametrize("H", [16, 24, 64, 128])
 def test_head_counts(cuda_device, H):
     B, S, D, N, K = 2, 10, 128, 64, 50
