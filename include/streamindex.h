@@ -92,6 +92,48 @@ int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, 
                        int64_t K, float softmax_scale, void* o, const int64_t* o_strides, float* lse,
                        const int64_t* lse_strides, void* stream);
 
+/*
+ * Fused indexer top-k that writes CSA attention index rows directly.
+ * Replaces flash_sparse/csa.py:149-179 (chunked indexer, window indices,
+ * "+S" offset of the compressed picks, int32 concat) and, for the same
+ * result without the [B,S,T] score matrix, csa.py:181-196 (indexer_score +
+ * build_csa_topk_idxs).
+ *
+ *   q, k_idx, weights, B..D, top_k, causal_ratio: as si_indexer_topk (no mask).
+ *   out_idx [B,S,n_win+top_k] int32, strides out_strides[3] (last must be 1):
+ *     column j < n_win: s - n_win + 1 + j, or -1 where negative;
+ *     column n_win + r: the r-th best legal key + idx_offset, -1 past the legal count.
+ *   out_scores: optional [B,S,top_k] fp32 contiguous (NULL = not written).
+ * Needs idx_offset + T < 2^31.
+ */
+int si_csa_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, const int64_t* k_strides,
+                        const void* weights, int w_dtype, const int64_t* w_strides, int64_t B, int64_t S,
+                        int64_t T, int64_t H, int64_t D, int64_t top_k, int64_t causal_ratio, int64_t n_win,
+                        int64_t idx_offset, int32_t* out_idx, const int64_t* out_strides, float* out_scores,
+                        void* stream);
+
+/*
+ * CSA attention index rows from a materialised score matrix.
+ * Replaces flash_sparse/csa.py:30-83 (build_csa_topk_idxs).
+ *
+ *   scores [B,S,T] fp32 with strides score_strides[3]; key t legal for row s iff
+ *   t < (s+1)/causal_ratio (causal_ratio 0: all legal) and its score is not -inf.
+ *   out_idx: as si_csa_indexer_topk.  Ties rank the smaller index first.
+ *   Supported: 1 <= top_k <= 2048.
+ */
+int si_csa_scores_topk(const float* scores, const int64_t* score_strides, int64_t B, int64_t S, int64_t T,
+                       int64_t top_k, int64_t causal_ratio, int64_t n_win, int64_t idx_offset, int32_t* out_idx,
+                       const int64_t* out_strides, void* stream);
+
+/*
+ * HCA attention index rows: window columns as above, then column n_win + i =
+ * i + idx_offset if m_prime*(i+1) - 1 <= s, else -1, for i < n_compressed.
+ * Replaces flash_sparse/hca.py:24-51 (build_hca_topk_idxs).
+ *   out_idx [B,S,n_win+n_compressed] int32, strides out_strides[3] (last must be 1).
+ */
+int si_hca_topk_idxs(int64_t B, int64_t S, int64_t n_win, int64_t n_compressed, int64_t m_prime,
+                     int64_t idx_offset, int32_t* out_idx, const int64_t* out_strides, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

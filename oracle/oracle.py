@@ -22,7 +22,9 @@ Reference semantics followed (file:line in the reference tree):
 * tie order (score desc, index asc): ``docs/streaming_topk.md:46-60``;
 * set-overlap recall: ``eval/test_v4_indexer_parity.py:164-199``;
 * sparse attention with sink: ``flash_sparse/reference.py:44-130``;
-  LSE: ``flash_sparse/triton/sparse_attn_fwd.py:148-177``.
+  LSE: ``flash_sparse/triton/sparse_attn_fwd.py:148-177``;
+* CSA / HCA attention index rows: ``flash_sparse/csa.py:30-83,176-179``,
+  ``flash_sparse/hca.py:24-51``, window ``flash_sparse/reference.py:460-475``.
 
 Parity status: every function here is pinned by ``tests/test_oracle.py``
 (brute force on tiny inputs, closed forms, invariants, and torch's own CPU
@@ -243,6 +245,48 @@ def np_sparse_attn(qf: np.ndarray, kvf: np.ndarray, sink: np.ndarray, idx: np.nd
     o = np.einsum("nhk,nkd->nhd", p, g) / den[..., None]
     lse = np.log(den) + mx
     return o, lse
+
+
+# ---------------------------------------------------------------------------
+# CSA / HCA attention index rows (integer work: numpy)
+# ---------------------------------------------------------------------------
+def window_idxs(rows: np.ndarray, n_win: int) -> np.ndarray:
+    """Sliding-window columns ``[n, n_win]`` (``flash_sparse/reference.py:460-475``):
+    column j of query s is ``s - n_win + 1 + j`` when that lies in ``[0, s]``, else -1."""
+    s = np.asarray(rows, dtype=np.int64)[:, None]
+    t = s - n_win + 1 + np.arange(n_win, dtype=np.int64)[None, :]
+    return np.where((t >= 0) & (t <= s), t, -1)
+
+
+def csa_idx_rows(comp_idx: np.ndarray, rows: np.ndarray, n_win: int, offset: int) -> np.ndarray:
+    """CSA attention index rows ``[n, n_win + K]`` from per-row compressed picks
+    (``flash_sparse/csa.py:76-83``, and ``:176-179`` for the chunked path):
+    window columns, then each pick ``+ offset`` (-1 stays -1)."""
+    comp = np.asarray(comp_idx, dtype=np.int64)
+    comp = np.where(comp >= 0, comp + offset, -1)
+    return np.concatenate([window_idxs(rows, n_win), comp], axis=1)
+
+
+def csa_scores_topk_rows(scores: np.ndarray, rows: np.ndarray, m: int, top_k: int, n_win: int,
+                         offset: int) -> np.ndarray:
+    """``build_csa_topk_idxs`` (``flash_sparse/csa.py:59-83``) for the given rows of one
+    batch: causal mask ``m(i+1)-1 <= s``, top-min(k,T) with ties by smaller index,
+    selected ``-inf`` -> -1, padding to ``top_k``, window + offset."""
+    rows = np.asarray(rows, dtype=np.int64)
+    lim = legal_limits(rows, scores.shape[1], m)
+    idx, val = topk(scores, lim, top_k)
+    idx = np.where(np.isneginf(val), -1, idx)
+    return csa_idx_rows(idx, rows, n_win, offset)
+
+
+def hca_idx_rows(rows: np.ndarray, n_win: int, n_comp: int, m_prime: int, offset: int) -> np.ndarray:
+    """HCA attention index rows ``[n, n_win + n_comp]`` (``flash_sparse/hca.py:40-51``):
+    window columns, then compressed entry i as ``i + offset`` where
+    ``m_prime·(i+1) - 1 <= s``, else -1."""
+    s = np.asarray(rows, dtype=np.int64)[:, None]
+    i = np.arange(n_comp, dtype=np.int64)[None, :]
+    comp = np.where(m_prime * (i + 1) - 1 <= s, i + offset, -1)
+    return np.concatenate([window_idxs(rows, n_win), comp], axis=1)
 
 
 # ---------------------------------------------------------------------------

@@ -5,7 +5,11 @@ Operators (hand-written HIP kernels behind the C ABI in
 
 * :func:`chunked_indexer_topk` — fused lightning-indexer score + exact top-k;
 * :func:`indexer_score`, :func:`indexer_score_topk`;
-* :func:`sparse_attn_fwd`, :func:`sparse_attn` — MQA sparse attention with sink.
+* :func:`sparse_attn_fwd`, :func:`sparse_attn` — MQA sparse attention with sink;
+* :func:`flash_csa_forward`, :func:`build_csa_topk_idxs`, :func:`csa_topk_idxs` —
+  the CSA composition (fused indexer → window + compressed index rows → attention);
+* :func:`flash_hca_forward`, :func:`build_hca_topk_idxs` — HCA (window + every
+  legal compressed entry).
 
 The same names are importable under the reference's module paths through the
 ``flash_sparse`` package (``flash_sparse.triton.chunked_indexer`` etc.).
@@ -13,6 +17,8 @@ The same names are importable under the reference's module paths through the
 
 from .indexer import chunked_indexer_topk, indexer_score, indexer_score_topk
 from .sparse_attn import sparse_attn, sparse_attn_fwd
+from .csa import build_csa_topk_idxs, csa_topk_idxs, flash_csa_forward
+from .hca import build_hca_topk_idxs, flash_hca_forward
 
 __version__ = "0.1.0"
 
@@ -22,4 +28,9 @@ __all__ = [
     "indexer_score_topk",
     "sparse_attn",
     "sparse_attn_fwd",
+    "flash_csa_forward",
+    "build_csa_topk_idxs",
+    "csa_topk_idxs",
+    "flash_hca_forward",
+    "build_hca_topk_idxs",
 ]

@@ -38,6 +38,10 @@ SIGNATURES = {
                                _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "si_indexer_score": (_I32, [_P, _I64P, _P, _I64P, _P, _I32, _I64P,
                                 _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P]),
+    "si_csa_indexer_topk": (_I32, [_P, _I64P, _P, _I64P, _P, _I32, _I64P, _I64, _I64, _I64, _I64, _I64,
+                                   _I64, _I64, _I64, _I64, _P, _I64P, _P, _P]),
+    "si_csa_scores_topk": (_I32, [_P, _I64P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P]),
+    "si_hca_topk_idxs": (_I32, [_I64, _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P]),
     "si_sparse_attn_fwd": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P,
                                   _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                   _P, _I64P, _P, _I64P, _P]),

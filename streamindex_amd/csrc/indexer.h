@@ -20,8 +20,16 @@ struct IndexerArgs {
   int B, S, T, H;
   int top_k;
   int ratio;  // > 0: legal iff t < (s+1)/ratio; 0: no causal bound
-  int64_t* out_idx;     // [B,S,top_k] contiguous
-  float* out_scores;    // [B,S,top_k] contiguous
+  int64_t* out_idx;     // [B,S,top_k] contiguous, or null when out_idx32 is set
+  float* out_scores;    // [B,S,top_k] contiguous, or null
+  // CSA index rows instead of out_idx: [B,S,n_win+top_k] int32 with batch /
+  // row strides o32sb / o32ss (columns contiguous).  Columns [0, n_win) hold
+  // the sliding window s-n_win+1 .. s (-1 below 0); columns n_win.. hold the
+  // selected keys plus idx_offset (-1 past the legal count).
+  int32_t* out_idx32;
+  int64_t o32sb, o32ss;
+  int n_win;
+  int idx_offset;
   float* scores;        // score kernel: [B,S,T]
   int64_t ssb, sss, sst;
 };

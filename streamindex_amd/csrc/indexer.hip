@@ -93,6 +93,36 @@ extern "C" int si_indexer_topk(const void* q, const int64_t* q_strides, const vo
   return dispatch_shape<true>(a, static_cast<int>(D), static_cast<hipStream_t>(stream));
 }
 
+extern "C" int si_csa_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx,
+                                   const int64_t* k_strides, const void* weights, int w_dtype,
+                                   const int64_t* w_strides, int64_t B, int64_t S, int64_t T, int64_t H,
+                                   int64_t D, int64_t top_k, int64_t causal_ratio, int64_t n_win,
+                                   int64_t idx_offset, int32_t* out_idx, const int64_t* out_strides,
+                                   float* out_scores, void* stream) {
+  IndexerArgs a{};
+  int rc = fill_common(a, q, q_strides, k_idx, k_strides, weights, w_dtype, w_strides, B, S, T, H, D);
+  if (rc) return rc;
+  if (top_k <= 0) return set_error(SI_ERR_INVALID, "top_k must be positive");
+  if (causal_ratio < 0 || causal_ratio > 0x7fffffff) return set_error(SI_ERR_INVALID, "bad causal_ratio");
+  if (n_win < 0 || n_win > 0x7fffffff) return set_error(SI_ERR_INVALID, "n_win must be non-negative");
+  if (idx_offset < 0 || idx_offset + T > 0x7fffffff)
+    return set_error(SI_ERR_UNSUPPORTED, "idx_offset + T must fit in int32");
+  if (!out_strides) return set_error(SI_ERR_INVALID, "null output strides");
+  if (!out_idx && B > 0 && S > 0) return set_error(SI_ERR_INVALID, "null output pointer");
+  if (out_strides[2] != 1) return set_error(SI_ERR_INVALID, "index rows must be contiguous");
+  a.top_k = static_cast<int>(top_k);
+  a.ratio = static_cast<int>(causal_ratio);
+  a.out_idx = nullptr;
+  a.out_scores = out_scores;
+  a.out_idx32 = out_idx;
+  a.o32sb = out_strides[0];
+  a.o32ss = out_strides[1];
+  a.n_win = static_cast<int>(n_win);
+  a.idx_offset = static_cast<int>(idx_offset);
+  if (a.B == 0 || a.S == 0) return SI_OK;
+  return dispatch_shape<true>(a, static_cast<int>(D), static_cast<hipStream_t>(stream));
+}
+
 extern "C" int si_indexer_score(const void* q, const int64_t* q_strides, const void* k_idx,
                                 const int64_t* k_strides, const void* weights, int w_dtype,
                                 const int64_t* w_strides, int64_t B, int64_t S, int64_t T, int64_t H,

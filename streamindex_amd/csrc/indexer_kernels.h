@@ -223,6 +223,15 @@ __device__ __forceinline__ void static_for(F& f) {
   static_for_impl<0, N>(f);
 }
 
+// Sliding-window columns of query s: column j holds key s - n_win + 1 + j,
+// or -1 where that is negative (flash_sparse/reference.py:460-475).
+__device__ __forceinline__ void write_window_cols(int32_t* orow, int s, int n_win, int lane) {
+  for (int j = lane; j < n_win; j += kWave) {
+    const int t = s - n_win + 1 + j;
+    orow[j] = t >= 0 ? t : -1;
+  }
+}
+
 __device__ __forceinline__ int legal_limit(const IndexerArgs& a, int s) {
   if (a.ratio > 0) {
     const int l = (s + 1) / a.ratio;
@@ -456,7 +465,16 @@ void indexer_topk_kernel(IndexerArgs a) {
 
   if (active) {
     const int64_t row = static_cast<int64_t>(b) * a.S + s;
-    sel.finish(a.out_idx + row * a.top_k, a.out_scores + row * a.top_k, lane);
+    TopkRowOut out{nullptr, a.out_scores ? a.out_scores + row * a.top_k : nullptr, nullptr, 0};
+    if (a.out_idx32) {
+      int32_t* orow = a.out_idx32 + b * a.o32sb + static_cast<int64_t>(s) * a.o32ss;
+      write_window_cols(orow, s, a.n_win, lane);
+      out.idx32 = orow + a.n_win;
+      out.off32 = a.idx_offset;
+    } else {
+      out.idx64 = a.out_idx + row * a.top_k;
+    }
+    sel.finish(out, lane);
   }
 }
 

@@ -110,6 +110,18 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&v)[E], int lane) {
   bitonic_levels<E, kWave * E, 2>(v, lane);
 }
 
+// Where finish() writes one row's sorted top-k.  Each pointer may be null.
+//   idx64 : int64 key indices, -1 past the held count;
+//   score : fp32 scores, -inf past the held count;
+//   idx32 : int32 key indices plus off32, -1 past the held count (the
+//           compressed-KV columns of a CSA attention index row).
+struct TopkRowOut {
+  int64_t* idx64;
+  float* score;
+  int32_t* idx32;
+  int32_t off32;
+};
+
 template <int C>
 struct WaveSelect {
   static constexpr int E = C / kWave;   // 64-key rows in the buffer
@@ -257,10 +269,10 @@ struct WaveSelect {
   // Keeping close to top_k keys leaves the most room and the highest floor.
   __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, compact_cmax()); }
 
-  // Sorted top_k of the row: indices (int64, -1 pad) and scores (fp32, -inf pad).
+  // Sorted top_k of the row, written through `out` (see TopkRowOut).
   // When top_k fits in half the buffer, the held keys are first cut to at
   // most C/2 (exactly top_k if more are held) so that only C/2 are sorted.
-  __device__ __forceinline__ void finish(int64_t* out_idx, float* out_score, int lane) {
+  __device__ __forceinline__ void finish(const TopkRowOut& out, int lane) {
     constexpr int HE = E / 2;
     if (top_k <= C / 2) {
       if (n > C / 2) compact_to(lane, top_k, top_k);
@@ -272,7 +284,7 @@ struct WaveSelect {
         v[j] = pos < n ? buf[pos] : 0ull;
       }
       wave_sort_desc<HE>(v, lane);
-      write_out<HE>(v, out_idx, out_score, lane);
+      write_out<HE>(v, out, lane);
     } else {
       if constexpr (E <= 32) {
         wave_lds_sync();
@@ -283,7 +295,7 @@ struct WaveSelect {
           v[j] = pos < n ? buf[pos] : 0ull;
         }
         wave_sort_desc<E>(v, lane);
-        write_out<E>(v, out_idx, out_score, lane);
+        write_out<E>(v, out, lane);
       }
     }
   }
@@ -291,16 +303,16 @@ struct WaveSelect {
   // Keys of rank lane*EE+j are staged through LDS in rank order so that the
   // global stores are contiguous across the wave.
   template <int EE>
-  __device__ __forceinline__ void write_out(const uint64_t (&v)[EE], int64_t* out_idx, float* out_score,
-                                            int lane) const {
+  __device__ __forceinline__ void write_out(const uint64_t (&v)[EE], const TopkRowOut& out, int lane) const {
     wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < EE; ++j) buf[lane * EE + j] = v[j];
     wave_lds_sync();
     for (int e = lane; e < top_k; e += kWave) {
       const uint64_t k = buf[e];
-      out_idx[e] = k ? static_cast<int64_t>(key_idx(k)) : int64_t(-1);
-      out_score[e] = k ? ord_to_f32(key_hi(k)) : -__builtin_inff();
+      if (out.idx64) out.idx64[e] = k ? static_cast<int64_t>(key_idx(k)) : int64_t(-1);
+      if (out.score) out.score[e] = k ? ord_to_f32(key_hi(k)) : -__builtin_inff();
+      if (out.idx32) out.idx32[e] = k ? static_cast<int32_t>(key_idx(k)) + out.off32 : int32_t(-1);
     }
   }
 };

@@ -40,7 +40,8 @@ def lib():
 
 def test_header_declares_expected_entries():
     names = _declared()
-    for n in ("si_indexer_topk", "si_indexer_score", "si_sparse_attn_fwd", "si_last_error", "si_abi_version"):
+    for n in ("si_indexer_topk", "si_indexer_score", "si_sparse_attn_fwd", "si_last_error", "si_abi_version",
+              "si_csa_indexer_topk", "si_csa_scores_topk", "si_hca_topk_idxs"):
         assert n in names
 
 
@@ -55,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.si_abi_version() == 1
+    assert lib.si_abi_version() == 2
     assert lib.si_indexer_topk_workspace_bytes(1, 1 << 20, 1 << 18, 64, 128, 512) == 0
 
 
@@ -101,6 +102,35 @@ def test_c_validation_codes_without_gpu(lib):
     assert rc == _lib.SI_ERR_INVALID
 
 
+def test_csa_hca_validation_codes_without_gpu(lib):
+    qs, ks, ws = _i64(8 * 64 * 128, 64 * 128, 128, 1), _i64(4 * 128, 128, 1), _i64(8 * 64, 64, 1)
+    os_ = _i64(8 * 24, 24, 1)
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+    # fused CSA rows: the +S offset must keep indices inside int32
+    rc = lib.si_csa_indexer_topk(fake, qs, fake, ks, fake, 0, ws, 1, 8, 4, 64, 128, 16, 4, 8, (1 << 31) - 2,
+                                 fake, os_, None, None)
+    assert rc == _lib.SI_ERR_UNSUPPORTED and b"int32" in lib.si_last_error()
+    rc = lib.si_csa_indexer_topk(fake, qs, fake, ks, fake, 0, ws, 1, 8, 4, 64, 128, 16, 4, -1, 8, fake, os_,
+                                 None, None)
+    assert rc == _lib.SI_ERR_INVALID and b"n_win" in lib.si_last_error()
+    rc = lib.si_csa_indexer_topk(fake, qs, fake, ks, fake, 0, ws, 1, 8, 4, 64, 128, 16, 4, 8, 8, fake,
+                                 _i64(8 * 24, 24, 2), None, None)
+    assert rc == _lib.SI_ERR_INVALID and b"contiguous" in lib.si_last_error()
+    # materialised-score CSA rows
+    ss = _i64(8 * 4, 4, 1)
+    rc = lib.si_csa_scores_topk(fake, ss, 1, 8, 4, 0, 4, 8, 8, fake, os_, None)
+    assert rc == _lib.SI_ERR_INVALID and b"top_k" in lib.si_last_error()
+    rc = lib.si_csa_scores_topk(fake, ss, 1, 8, 4, 4096, 4, 8, 8, fake, os_, None)
+    assert rc == _lib.SI_ERR_UNSUPPORTED
+    rc = lib.si_csa_scores_topk(fake, ss, 1, 0, 4, 16, 4, 8, 8, None, os_, None)  # empty: no launch
+    assert rc == _lib.SI_OK
+    # HCA rows
+    rc = lib.si_hca_topk_idxs(1, 8, 4, 2, 0, 8, fake, os_, None)
+    assert rc == _lib.SI_ERR_INVALID and b"m_prime" in lib.si_last_error()
+    rc = lib.si_hca_topk_idxs(1, 0, 4, 2, 4, 0, None, os_, None)
+    assert rc == _lib.SI_OK
+
+
 def test_python_layer_errors_on_cpu_tensors():
     from streamindex_amd import chunked_indexer_topk, indexer_score, sparse_attn_fwd
 
@@ -114,6 +144,18 @@ def test_python_layer_errors_on_cpu_tensors():
     with pytest.raises(AssertionError):
         sparse_attn_fwd(torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16), torch.zeros(1, 4, 64, dtype=torch.bfloat16),
                         torch.zeros(16), torch.zeros(1, 2, 4, dtype=torch.int64))
+    from streamindex_amd import build_csa_topk_idxs, flash_csa_forward, flash_hca_forward
+
+    with pytest.raises(AssertionError):  # T != n_compressed (csa.py:56)
+        build_csa_topk_idxs(torch.zeros(1, 8, 2), 4, 2, seq_len=8, n_compressed=3, m=4, device="cpu")
+    with pytest.raises(AssertionError):  # CPU scores
+        build_csa_topk_idxs(torch.zeros(1, 8, 2), 4, 2, seq_len=8, n_compressed=2, m=4, device="cpu")
+    with pytest.raises(AssertionError):  # kv shape (csa.py:128)
+        flash_csa_forward(torch.zeros(1, 8, 4, 32, dtype=torch.bfloat16), torch.zeros(1, 7, 32, dtype=torch.bfloat16),
+                          torch.zeros(1, 2, 32, dtype=torch.bfloat16), q, k, w, torch.zeros(4), n_win=4, top_k=2)
+    with pytest.raises(AssertionError):
+        flash_hca_forward(torch.zeros(1, 8, 4, 32, dtype=torch.bfloat16), torch.zeros(1, 8, 32, dtype=torch.bfloat16),
+                          torch.zeros(1, 2, 32, dtype=torch.bfloat16), torch.zeros(4), n_win=4, m_prime=4)
 
 
 def test_error_mapping():
@@ -139,9 +181,13 @@ def test_reference_import_paths():
     from flash_sparse.triton.chunked_indexer import chunked_indexer_topk
     from flash_sparse.triton.indexer_score import indexer_score, indexer_score_topk
     from flash_sparse.triton.sparse_attn_fwd import sparse_attn_fwd
+    from flash_sparse.csa import build_csa_topk_idxs, flash_csa_forward
+    from flash_sparse.hca import build_hca_topk_idxs, flash_hca_forward
 
     import streamindex_amd as si
 
+    assert flash_csa_forward is si.flash_csa_forward and build_csa_topk_idxs is si.build_csa_topk_idxs
+    assert flash_hca_forward is si.flash_hca_forward and build_hca_topk_idxs is si.build_hca_topk_idxs
     assert chunked_indexer_topk is si.chunked_indexer_topk
     assert indexer_score is si.indexer_score and indexer_score_topk is si.indexer_score_topk
     assert sparse_attn_fwd is si.sparse_attn_fwd and ft.sparse_attn is si.sparse_attn
