@@ -16,7 +16,11 @@ Printed (one JSON line, rank 0):
   parity         recall vs the CPU oracle on sampled rows
   cpu_baseline   the CPU oracle on a bounded row sample, extrapolated
   extra          S=1M indexer time (config[4] indexer stage), sparse-attn fwd
-                 at config[3] with its HBM roofline
+                 at config[3] with its HBM roofline, and the end-to-end CSA
+                 forward (flash_csa_forward: fused indexer -> int32 window +
+                 compressed index rows -> sparse attention, 64 heads, d=576,
+                 n_win=128) at S=64K and at S=1M (config[4]) with its stage
+                 split, peak HBM and sampled-row recall against the oracle
 """
 
 from __future__ import annotations
@@ -33,7 +37,8 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from streamindex_amd import chunked_indexer_topk, sparse_attn_fwd, synth  # noqa: E402
+from streamindex_amd import chunked_indexer_topk, csa_topk_idxs, flash_csa_forward, sparse_attn, sparse_attn_fwd  # noqa: E402,E501
+from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
@@ -87,8 +92,8 @@ def indexer_parity_and_cpu(q, k, w, idx, sc, ratio, top_k, nrows, seed=0):
     local = np.arange(len(rows), dtype=np.int64)
     O.lib()
     t0 = time.perf_counter()
-    scores = O.indexer_scores(qb, kb, wb, local)  # rows' own q/w are packed densely
     lim = O.legal_limits(rows, T, ratio)
+    scores = O.indexer_scores(qb, kb, wb, local, lim=lim)  # rows' own q/w are packed densely
     ref_idx, _ = O.topk(scores, lim, top_k)
     cpu_s = time.perf_counter() - t0
     got = idx[0].cpu().numpy()[rows]
@@ -140,6 +145,85 @@ def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None):
     return dict(ms=ms, flops=flops, unique_bytes=unique_bytes, nvalid=nvalid)
 
 
+def csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m, nrows, seed=3):
+    """Recall of the compressed picks of `nrows` sampled rows against the oracle."""
+    from oracle import oracle as O
+
+    S = qi.shape[1]
+    T = ki.shape[1]
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(S, size=min(nrows, S), replace=False)).astype(np.int64)
+    sel = torch.from_numpy(rows).to(qi.device)
+    lim = O.legal_limits(rows, T, m)
+    sc = O.indexer_scores(_bits(qi[0, sel]), _bits(ki[0]), w[0, sel].float().cpu().numpy(),
+                          np.arange(len(rows), dtype=np.int64), lim=lim)
+    ref_idx, _ = O.topk(sc, lim, top_k)
+    got = rows_gpu[0, sel, n_win:].long().cpu().numpy()
+    got = np.where(got >= 0, got - S, -1)
+    rec = O.set_overlap_recall(ref_idx, got)
+    return {"rows": int(len(rows)), "recall_mean": float(rec.mean()), "recall_min": float(rec.min())}
+
+
+def csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=8, seed=4):
+    """Max |o - o_ref| of the attention output on `nrows` sampled rows (oracle over the GPU's index rows)."""
+    from oracle import oracle as O
+
+    S, H, D = q.shape[1], q.shape[2], q.shape[3]
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(S, size=min(nrows, S), replace=False)).astype(np.int64)
+    sel = torch.from_numpy(rows).to(q.device)
+    idx = rows_gpu[0, sel].long()
+    kv_full = torch.cat([kv[0], kvc[0]], dim=0)
+    uniq = torch.unique(idx[idx >= 0])
+    remap = torch.where(idx >= 0, torch.searchsorted(uniq, idx.clamp(min=0)), torch.full_like(idx, -1))
+    o = sparse_attn(q[:, sel], torch.cat([kv, kvc], dim=1), sink, rows_gpu[:, sel], None)
+    ro, _ = O.sparse_attn_rows(_bits(q[0, sel]), _bits(kv_full[uniq]), sink.cpu().numpy(), remap.cpu().numpy(),
+                               D ** -0.5)
+    return float(np.abs(o[0].float().cpu().numpy() - ro).max())
+
+
+def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m=4, n_win=128, top_k=512):
+    """flash_csa_forward at V4-Flash dims; returns timings, stage split, peak HBM and parity."""
+    dev = torch.device("cuda:0")
+    qi, ki, w = synth.indexer_inputs(1, S, H_I, D_I, ratio=m, seed=2026, device=dev)
+    q, kv, kvc, sink = synth.csa_attn_inputs(1, S, n_h, d, S // m, seed=2027, device=dev)
+    fn = lambda: flash_csa_forward(q, kv, kvc, qi, ki, w, sink, n_win=n_win, top_k=top_k, m=m)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    peak = _peak_gib(fn)
+    stream = torch.cuda.current_stream(dev)
+    ms = _events_time(fn, steps, stream)
+    # stage split of one call (same three steps flash_csa_forward runs)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record(stream)
+    rows_gpu = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m, seq_len=S)
+    ev[1].record(stream)
+    kv_full = torch.cat([kv, kvc], dim=1)
+    ev[2].record(stream)
+    o = sparse_attn(q, kv_full, sink, rows_gpu, None)
+    ev[3].record(stream)
+    torch.cuda.synchronize()
+    del o, kv_full
+    nvalid = float((rows_gpu >= 0).sum().item())
+    res = {
+        "S": S, "T": S // m, "n_h": n_h, "d": d, "n_win": n_win, "top_k": top_k,
+        "ms": ms, "peak_hbm_gib": peak,
+        "indexer_ms": ev[0].elapsed_time(ev[1]), "concat_ms": ev[1].elapsed_time(ev[2]),
+        "attn_ms": ev[2].elapsed_time(ev[3]),
+        "indexer_flops": synth.indexer_flops(S, S // m, H_I, D_I, m),
+        "attn_flops": 4.0 * n_h * d * nvalid,
+    }
+    res["indexer_tflops"] = res["indexer_flops"] / (res["indexer_ms"] * 1e-3) / 1e12
+    res["attn_tflops"] = res["attn_flops"] / (res["attn_ms"] * 1e-3) / 1e12
+    if parity_rows > 0:
+        res["parity"] = csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m, parity_rows)
+        res["attn_max_abs_err"] = csa_attn_check(q, kv, kvc, sink, rows_gpu)
+    del q, kv, kvc, qi, ki, w, rows_gpu
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,6 +239,11 @@ def main():
     ap.add_argument("--no-attn", action="store_true", help="skip the sparse-attention measurement")
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
     ap.add_argument("--only-attn", action="store_true", help="sparse-attention timing only (for profilers)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end CSA forward measurements")
+    ap.add_argument("--e2e-parity-rows", type=int, default=1024,
+                    help="sampled rows for the S=1M end-to-end recall check (config[4] asks 1024)")
+    ap.add_argument("--only-e2e", type=int, default=0, metavar="S",
+                    help="end-to-end CSA forward timing at sequence length S only (for profilers)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run 5 plain device copies of MIB MiB (scales HBM byte counters) and exit")
     args = ap.parse_args()
@@ -166,6 +255,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_mib": args.calibrate_copy, "launches": 5}), flush=True)
+        return
+    if args.only_e2e:
+        re_ = run_csa_e2e(args.only_e2e, args.steps, args.warmup, 0)
+        print(json.dumps({k: v for k, v in re_.items() if not isinstance(v, dict)}), flush=True)
         return
     if args.only_attn:
         ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup)
@@ -218,6 +311,12 @@ def main():
         extra["sparse_attn_unique_gbps"] = ra["unique_bytes"] / (ra["ms"] * 1e-3) / 1e9
         extra["sparse_attn_hbm_frac"] = extra["sparse_attn_unique_gbps"] / PEAK_HBM_GBPS
         extra["sparse_attn_mfma_frac"] = extra["sparse_attn_tflops"] / PEAK_BF16_TFLOPS
+
+    if not args.no_e2e:
+        print("[bench] end-to-end CSA forward S=64K", file=sys.stderr, flush=True)
+        extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256)
+        print("[bench] end-to-end CSA forward S=1M (config[4])", file=sys.stderr, flush=True)
+        extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

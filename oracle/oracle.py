@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
         I = ctypes.c_int64
         L.oracle_indexer_scores.argtypes = [P, P, P, I, I, I, I, P, I, P]
         L.oracle_indexer_scores.restype = None
+        L.oracle_indexer_scores_lim.argtypes = [P, P, P, I, I, I, I, P, I, P, P]
+        L.oracle_indexer_scores_lim.restype = None
         L.oracle_indexer_scores_f32.argtypes = [P, P, P, I, I, I, I, P, I, P]
         L.oracle_indexer_scores_f32.restype = None
         L.oracle_topk.argtypes = [P, I, I, P, P, I, P, P]
@@ -95,11 +97,13 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
 # Indexer (C oracle)
 # ---------------------------------------------------------------------------
 def indexer_scores(q_bits: np.ndarray, k_bits: np.ndarray, w: np.ndarray, rows: Optional[np.ndarray] = None,
-                   precision: str = "f64") -> np.ndarray:
+                   precision: str = "f64", lim: Optional[np.ndarray] = None) -> np.ndarray:
     """Scores ``I(s, t)`` for the selected query rows of ONE batch.
 
     q_bits [S,H,D] uint16 (bf16 bits), k_bits [T,D] uint16, w [S,H] float32.
     Returns [len(rows), T] float64 (or float32 with ``precision='f32'``).
+    With ``lim`` (f64 only), row r is scored for keys t < lim[r] only and holds
+    NaN beyond (those keys are illegal and never read by the top-k).
     """
     S, H, D = q_bits.shape
     T = k_bits.shape[0]
@@ -109,8 +113,14 @@ def indexer_scores(q_bits: np.ndarray, k_bits: np.ndarray, w: np.ndarray, rows: 
     rows = np.arange(S, dtype=np.int64) if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
     if precision == "f64":
         out = np.empty((len(rows), T), dtype=np.float64)
-        lib().oracle_indexer_scores(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows), len(rows),
-                                    _ptr(out))
+        if lim is None:
+            lib().oracle_indexer_scores(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows), len(rows),
+                                        _ptr(out))
+        else:
+            lim = np.ascontiguousarray(lim, dtype=np.int64)
+            assert lim.shape == rows.shape
+            lib().oracle_indexer_scores_lim(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows),
+                                            len(rows), _ptr(lim), _ptr(out))
     else:
         out = np.empty((len(rows), T), dtype=np.float32)
         lib().oracle_indexer_scores_f32(_ptr(q_bits), _ptr(k_bits), _ptr(w), S, T, H, D, _ptr(rows), len(rows),

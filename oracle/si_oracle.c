@@ -31,16 +31,33 @@ static inline float bf16_to_f32(uint16_t b) {
 }
 
 /*
- * Scores of `nrows` query rows against all T keys (one batch).
+ * Scores of `nrows` query rows against the keys of one batch.
  *   q   [S, H, D] bf16 bits       k [T, D] bf16 bits       w [S, H] fp32
  *   rows[i] selects the query row; out [nrows, T] (double).
+ *   lim: NULL, or per row the number of leading keys to score (the causal
+ *        limit); out[r, t] for t >= lim[r] is set to NaN (never a legal key).
  * Follows reference.py:165-168: relu per head, then the weighted head sum.
+ * Every (row, key) value is accumulated in a fixed order (d ascending inside
+ * a head, heads ascending); keys are processed KB at a time so the compiler
+ * vectorises across keys without reordering any single key's sums.
  */
-void oracle_indexer_scores(const uint16_t* q, const uint16_t* k, const float* w, int64_t S, int64_t T,
-                           int64_t H, int64_t D, const int64_t* rows, int64_t nrows, double* out) {
+#define SI_KB 8
+typedef double si_v4d __attribute__((vector_size(32)));
+typedef long long si_v4l __attribute__((vector_size(32)));
+void oracle_indexer_scores_lim(const uint16_t* q, const uint16_t* k, const float* w, int64_t S, int64_t T,
+                               int64_t H, int64_t D, const int64_t* rows, int64_t nrows, const int64_t* lim,
+                               double* out) {
   (void)S;
-  double* kd = (double*)malloc(sizeof(double) * (size_t)(T * D));
-  for (int64_t i = 0; i < T * D; ++i) kd[i] = (double)bf16_to_f32(k[i]);
+  const int64_t nb = (T + SI_KB - 1) / SI_KB;
+  /* keys transposed in blocks of SI_KB: kb[(b*D + d)*SI_KB + j] = k[b*SI_KB + j, d] (0 past T) */
+  double* kb = (double*)aligned_alloc(32, sizeof(double) * (size_t)(nb * D * SI_KB + 4));
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < nb; ++b)
+    for (int64_t d = 0; d < D; ++d)
+      for (int64_t j = 0; j < SI_KB; ++j) {
+        const int64_t t = b * SI_KB + j;
+        kb[(b * D + d) * SI_KB + j] = t < T ? (double)bf16_to_f32(k[t * D + d]) : 0.0;
+      }
 #pragma omp parallel
   {
     double* qd = (double*)malloc(sizeof(double) * (size_t)(H * D));
@@ -49,21 +66,41 @@ void oracle_indexer_scores(const uint16_t* q, const uint16_t* k, const float* w,
       const int64_t s = rows[r];
       for (int64_t i = 0; i < H * D; ++i) qd[i] = (double)bf16_to_f32(q[s * H * D + i]);
       const float* ws = w + s * H;
-      for (int64_t t = 0; t < T; ++t) {
-        const double* kt = kd + t * D;
-        double acc = 0.0;
+      int64_t L = lim ? lim[r] : T;
+      L = L < 0 ? 0 : (L > T ? T : L);
+      const int64_t nbr = (L + SI_KB - 1) / SI_KB;
+      for (int64_t b = 0; b < nbr; ++b) {
+        const si_v4d* kblk = (const si_v4d*)(kb + b * D * SI_KB);
+        si_v4d acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = acc0;
+        const si_v4d zero = acc0;
         for (int64_t h = 0; h < H; ++h) {
           const double* qh = qd + h * D;
-          double dot = 0.0;
-          for (int64_t d = 0; d < D; ++d) dot += qh[d] * kt[d];
-          if (dot > 0.0) acc += (double)ws[h] * dot;
+          si_v4d dot0 = zero, dot1 = zero;
+          for (int64_t d = 0; d < D; ++d) {
+            const double qv = qh[d];
+            dot0 += qv * kblk[2 * d];
+            dot1 += qv * kblk[2 * d + 1];
+          }
+          const double wh = (double)ws[h];
+          /* relu: the weighted term where dot > 0, else +0.0 (bit mask) */
+          acc0 += (si_v4d)((si_v4l)(wh * dot0) & (dot0 > zero));
+          acc1 += (si_v4d)((si_v4l)(wh * dot1) & (dot1 > zero));
         }
-        out[r * T + t] = acc;
+        for (int j = 0; j < SI_KB; ++j) {
+          const int64_t t = b * SI_KB + j;
+          if (t < L) out[r * T + t] = j < 4 ? acc0[j] : acc1[j - 4];
+        }
       }
+      for (int64_t t = L; t < T; ++t) out[r * T + t] = NAN;
     }
     free(qd);
   }
-  free(kd);
+  free(kb);
+}
+
+void oracle_indexer_scores(const uint16_t* q, const uint16_t* k, const float* w, int64_t S, int64_t T,
+                           int64_t H, int64_t D, const int64_t* rows, int64_t nrows, double* out) {
+  oracle_indexer_scores_lim(q, k, w, S, T, H, D, rows, nrows, NULL, out);
 }
 
 /* Same as above in float accumulation (the reference's working precision). */

@@ -54,6 +54,26 @@ def sparse_attn_inputs(B: int, S: int, H: int, D: int, N_kv: int, *, seed: int =
     return q.to(device), kv.to(device), sink.to(device)
 
 
+def csa_attn_inputs(B: int, S: int, H: int, D: int, T: int, *, seed: int = 2027, device="cuda",
+                    scale: float = 1.0):
+    """Attention-side CSA inputs: ``(q [B,S,H,D], kv [B,S,D], kv_compressed [B,T,D])``
+    bf16 ~ N(0,1)·scale and ``attn_sink [H]`` fp32 ~ N(0,1).  Large tensors are
+    drawn on the device and scaled in place (no second copy at S = 1M, where q
+    alone is 72 GiB)."""
+    device = torch.device(device)
+    on_dev = device.type == "cuda" and B * S * H * D > CPU_DRAW_LIMIT
+    g = _gen(device, seed, on_dev)
+    where = device if on_dev else "cpu"
+    out = []
+    for shape in ((B, S, H, D), (B, S, D), (B, T, D)):
+        t = torch.randn(*shape, generator=g, device=where, dtype=torch.bfloat16)
+        if scale != 1.0:
+            t.mul_(scale)
+        out.append(t.to(device))
+    out.append(torch.randn(H, generator=g, device=where, dtype=torch.float32).to(device))
+    return tuple(out)
+
+
 def causal_random_topk(B: int, S: int, K: int, ratio: int, *, seed: int = 7, device="cuda") -> torch.Tensor:
     """Random distinct causal-legal compressed indices per row (``-1`` past the
     legal count), for attention tests that do not run the indexer first."""
@@ -99,5 +119,6 @@ def _check_legal_pairs():  # pragma: no cover - used by tests
     return True
 
 
-__all__ = ["indexer_inputs", "sparse_attn_inputs", "causal_random_topk", "legal_pairs", "indexer_flops"]
+__all__ = ["indexer_inputs", "sparse_attn_inputs", "csa_attn_inputs", "causal_random_topk", "legal_pairs",
+           "indexer_flops"]
 del math

@@ -103,8 +103,8 @@ def check_indexer(q, k, w, top_k, got_idx, got_val, *, causal_ratio=None, mask=N
         qb = bf16_bits(q[b])
         kb = bf16_bits(k[b])
         wb = w[b].float().cpu().numpy()
-        sc = O.indexer_scores(qb, kb, wb, rows)
         lim = O.legal_limits(rows, T, causal_ratio)
+        sc = O.indexer_scores(qb, kb, wb, rows, lim=lim)
         mrows = None
         if mask is not None:
             mrows = mask[b].cpu().numpy().astype(np.uint8)[rows]

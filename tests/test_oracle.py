@@ -71,6 +71,24 @@ def test_scores_brute_force_tiny():
                        ref, rtol=0, atol=1e-12)
 
 
+def test_scores_brute_force_key_blocks_and_causal_limit():
+    # T not a multiple of the oracle's 8-key vector blocks; D, H beyond the tiny case
+    rng = np.random.default_rng(11)
+    S, H, D, T = 5, 3, 16, 21
+    qb, kb = _rand_bf16(rng, (S, H, D)), _rand_bf16(rng, (T, D))
+    w = rng.standard_normal((S, H)).astype(np.float32)
+    ref = _brute_scores(O.bf16_bits_to_f64(qb), O.bf16_bits_to_f64(kb), w.astype(np.float64))
+    full = O.indexer_scores(qb, kb, w)
+    assert np.allclose(full, ref, rtol=0, atol=1e-12)
+    rows = np.array([4, 0, 2, 3])
+    lim = np.array([0, 7, 21, 9])
+    got = O.indexer_scores(qb, kb, w, rows, lim=lim)
+    for r, (s, L) in enumerate(zip(rows, lim)):
+        # the legal prefix is bit-identical to the unlimited scores; the rest is NaN
+        assert np.array_equal(got[r, :L].view(np.uint64), full[s, :L].view(np.uint64))
+        assert np.isnan(got[r, L:]).all()
+
+
 def test_scores_match_torch_reference_formula():
     # reference.py:165-168 executed by torch on the CPU in fp32
     rng = np.random.default_rng(2)
