@@ -61,6 +61,42 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int mask)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
+// Value of lane (this lane ^ LX) for LX in {1, 2, 4, 8, 16, 32}, without LDS:
+// DPP quad permutes for 1 and 2, two bank-masked row shifts for 4, a row
+// rotation by 8 for 8, and v_permlane{16,32}_swap (plus a select by the lane's
+// half) for 16 and 32.  A swap(x, x) returns {vdst', src'}: lanes of the upper
+// row / half find their partner in vdst', the others in src'.
+template <int LX>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t x) {
+  const int xi = static_cast<int>(x);
+  if constexpr (LX == 1) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+  } else if constexpr (LX == 2) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+  } else if constexpr (LX == 4) {
+    const int t = __builtin_amdgcn_update_dpp(xi, xi, 0x114, 0xf, 0xA, false);  // row_shr:4 into banks 1,3
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(t, xi, 0x104, 0xf, 0x5, false));  // row_shl:4 into 0,2
+  } else if constexpr (LX == 8) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0x128, 0xf, 0xf, false));  // row_ror:8
+  } else if constexpr (LX == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return __builtin_amdgcn_inverse_ballot_w64(0xFFFF0000FFFF0000ull) ? static_cast<uint32_t>(r[0])
+                                                                       : static_cast<uint32_t>(r[1]);
+  } else {
+    static_assert(LX == 32, "lane xor distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __builtin_amdgcn_inverse_ballot_w64(0xFFFFFFFF00000000ull) ? static_cast<uint32_t>(r[0])
+                                                                       : static_cast<uint32_t>(r[1]);
+  }
+}
+
+template <int LX>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v) {
+  const uint32_t lo = lane_xor_u32<LX>(static_cast<uint32_t>(v));
+  const uint32_t hi = lane_xor_u32<LX>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // Half-wave exchange (v_permlane32_swap): returns {a', b'} where a' and b'
 // together hold a's and b's 32-lane halves regrouped so that, in every lane,
 // a' and b' come from the same source register (a or b) and from the two

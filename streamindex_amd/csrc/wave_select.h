@@ -61,7 +61,7 @@ __device__ __forceinline__ void bitonic_stage(uint64_t (&v)[E], int lane) {
     constexpr uint64_t KM = keep_max_lane_mask<E, N, SIZE, LX>();
     uint64_t o[E];
 #pragma unroll
-    for (int j = 0; j < E; ++j) o[j] = shfl_xor_u64(v[j], lane, LX);
+    for (int j = 0; j < E; ++j) o[j] = lane_xor_u64<LX>(v[j]);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       // take the partner's key iff it is larger and this lane keeps the max, or
