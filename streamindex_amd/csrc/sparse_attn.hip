@@ -9,14 +9,16 @@
 //   p_j = e^{scale·q[s,h]·kv[idx_j] - m},  idx_j = -1 (or out of range) masked,
 //   lse[s,h] = log(Σ_j p_j + e^{sink_h - m}) + m.
 //
-// Design (one query row and up to 64 heads per workgroup of 4 waves):
+// Design (one query row and up to 64 heads per workgroup of 8 waves: four
+// S^T/softmax "producer" waves and four P.V "consumer" waves, one of each per
+// SIMD, so the matrix cores of a SIMD alternate between the two roles):
 //   * The row's top-k KV rows are gathered 32 at a time straight from L2/HBM
-//     into a 3-slot LDS ring with global_load_lds (no staging registers), two
-//     tiles ahead of use; each row is read once per query for all heads.
+//     into a 4-slot LDS ring with global_load_lds (no staging registers),
+//     three tiles ahead of use; each row is read once per query for all heads.
 //     Rows are stored key-major with a per-key XOR swizzle of the 16-byte
 //     chunks so that both LDS read patterns below are bank-conflict-free.
 //   * S^T = K·Q^T (v_mfma_f32_16x16x32_bf16, keys on M, heads on N), split
-//     across the waves by head (16 heads per wave, Q^T in VGPRs).  Each lane
+//     across the producers by head (16 heads per wave, Q^T in VGPRs).  Each lane
 //     then holds one head, so the online-softmax max and sum are in-lane plus
 //     two xor exchanges.  The reference maximum is raised only when the tile
 //     maximum exceeds it by 2^64 (the result is unchanged up to rounding), so
@@ -25,8 +27,10 @@
 //   * P^T (bf16) and the per-head rescale factors of all 64 heads are
 //     exchanged through a small double-buffered LDS area; one barrier per
 //     tile.
-//   * O^T = V^T·P^T, split across the waves by output dimension (the 16-dim
-//     blocks are dealt round-robin), so every V element is read from LDS once.
+//   * O^T = V^T·P^T, split across the consumers by output dimension (the
+//     16-dim blocks are dealt round-robin), so every V element is read from
+//     LDS once.  The consumers also issue the KV gathers and run the index
+//     pipeline, so each role needs at most ~210 VGPRs and two waves fit a SIMD.
 //     The V^T A-fragments are read from the key-major tile with
 //     ds_read_b64_tr_b16 (two transposing reads give a lane 8 keys of one
 //     dimension); the P^T B-fragments use the key order of the score
@@ -184,48 +188,13 @@ __device__ __forceinline__ void reg_tie(T& x) {
   asm volatile("" : "+v"(x));
 }
 
-// Issue order of the pipelined LDS reads of one tile iteration (all from
-// inline asm, so the wait counts are exact).  Step u (u < 4 MBW) runs the
-// P.V MFMA of V^T block u/4 and head block u%4 and, for u < KS with QK, the
-// two S^T MFMAs of k-step u.  Issued first: 4 P^T fragments, V^T blocks 0
-// and 1 (two reads each), the S^T operands of k-steps 0..QPD-1 (two reads
-// each); after the MFMAs of step u: the S^T operands of k-step u + QPD and,
-// when u % 4 == 0, V^T block u/4 + 2.
-template <int KS, int MBW, bool QK>
-struct AttnSched {
-  static constexpr int QPD = KS < 4 ? KS : 4;
-  static constexpr int NSTEP = 4 * MBW;  // >= KS for every supported D
-  static constexpr int PRE_TR = MBW > 1 ? 4 : 2;
-  static constexpr int PRE = 4 + PRE_TR + (QK ? 2 * QPD : 0);
-  static constexpr bool kq_at(int u) { return QK && u + QPD < KS; }
-  static constexpr bool tr_at(int u) { return u % 4 == 0 && u / 4 + 2 < MBW; }
-  static constexpr int issued_before(int u) {
-    int n = PRE;
-    for (int i = 0; i < u; ++i) n += (kq_at(i) ? 2 : 0) + (tr_at(i) ? 2 : 0);
-    return n;
-  }
-  // issue index of the second read of S^T k-step k / of V^T block j
-  static constexpr int kq_last(int k) { return k < QPD ? 4 + PRE_TR + 2 * k + 1 : issued_before(k - QPD) + 1; }
-  static constexpr int tr_last(int j) {
-    return j < 2 ? 4 + 2 * j + 1 : issued_before(4 * (j - 2)) + (kq_at(4 * (j - 2)) ? 2 : 0) + 1;
-  }
-  // LDS reads that may stay outstanding before step u's MFMAs (-1: no wait)
-  static constexpr int wait_at(int u) {
-    int need = -1;
-    if (QK && u < KS && kq_last(u) > need) need = kq_last(u);
-    if (u % 4 == 0 && tr_last(u / 4) > need) need = tr_last(u / 4);
-    if (u == 0 && need < 3) need = 3;  // the P^T fragments
-    if (need < 0) return -1;
-    const int w = issued_before(u) - 1 - need;
-    return w < 15 ? w : 15;  // lgkmcnt field limit (a lower count only waits longer)
-  }
-  // step at which softmax stage k (of NSM) runs: spread over the steps that
-  // follow the last S^T MFMA
-  static constexpr int sm_step(int k, int NSM) { return KS + k * (NSTEP - KS) / NSM; }
-};
+// Threads of a workgroup: kAttnWaves S^T / softmax waves ("producers", 16
+// heads each) and kAttnWaves P.V waves ("consumers", 16-dim output blocks
+// dealt round-robin), one of each per SIMD.
+constexpr int kAttnThreads = 2 * kAttnWaves * 64;
 
 template <int D, bool IDX64>
-__global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
   using SH = AttnShape<D>;
   constexpr int KS = SH::KS;
   constexpr int MBW = SH::MBW;
@@ -239,8 +208,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[2 * kAttnRing][2 * kAttnTK];  // raw index words
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  __builtin_assume(wave >= 0 && wave < kAttnWaves);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __builtin_assume(wave_all >= 0 && wave_all < 2 * kAttnWaves);
+  const bool producer = wave_all < kAttnWaves;
+  const int wave = producer ? wave_all : wave_all - kAttnWaves;  // index within the role
+  __builtin_assume(wave >= 0 && wave < kAttnWaves);  // lets per-copy bounds fold at compile time
   const int g = lane >> 4;     // lane group 0..3
   const int i16 = lane & 15;
   const int s = blockIdx.x % a.S;
@@ -248,432 +220,403 @@ __global__ __launch_bounds__(kAttnWaves * 64) void sparse_attn_fwd_kernel(Sparse
   const int b = rest % a.B;
   const int hg = rest / a.B;
   const int hbase = hg * 64;
-  const int hq = hbase + wave * 16 + i16;  // this lane's head in S^T
-  const bool hvalid = hq < a.H;
-  // with no KV rows every key is masked: the loop is skipped
+  // with no KV rows every key is masked: the tile loop is skipped
   const int ntiles = a.N > 0 ? (a.K + kAttnTK - 1) / kAttnTK : 0;
 
-  const char* idx_row = static_cast<const char*>(a.idx) +
-                        (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
-  const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+  // Tile protocol (one barrier per tile).  Iteration `it`: the consumers
+  // compute P.V of tile it while the producers compute S^T + softmax of tile
+  // it+1 and publish its P^T and rescale factors; tile t lives in ring slot
+  // t % 4 and its P^T in p_lds[t % 2].  The consumers issue the copies of
+  // tile it+3 at the start of the iteration into the slot of tile it-1
+  // (finished by every wave in iteration it-1); they must land by the end of
+  // iteration it+1, two iterations of gather latency.  The first consumer
+  // wave copies the raw indices of tile it+6 at the start and publishes those
+  // of tile it+5 (copied one iteration earlier) before the barrier.
 
-  // Key indices of tile `t`: wave 0 copies the raw index words into
-  // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
-  // no loop-carried load result forces an early wait), and after its next
-  // full wait reads them back, validates them and publishes validity and row
-  // byte offsets to ring slot t % 3 for every wave.
-  auto load_idx = [&](int t) {
-    // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
-    int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
-    j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
-    const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
-                                     (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
-  };
-  auto store_idx = [&](int t) {
-    const int slot = t % kAttnRing;
-    const int rslot = t % (2 * kAttnRing);
-    if (lane < kAttnTK) {
-      const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
-                                                       idxraw_lds[rslot][2 * lane])
-                                : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
-      const int j = t * kAttnTK + lane;
-      const bool ok = j < a.K && raw >= 0 && raw < a.N;
-      bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
-      rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
+  if (producer) {
+    // ======================= S^T + online softmax ==========================
+    const int hq = hbase + wave * 16 + i16;  // this lane's head
+    const bool hvalid = hq < a.H;
+    bf16x8 qf[KS];
+    {
+      const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
     }
-  };
-  // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
-  // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
-  // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
-  // source is kv + 16 (rowoff16[key] + dcoff).
-  int dkey[SH::LPT], dcoff[SH::LPT];
-#pragma unroll
-  for (int i = 0; i < SH::LPT; ++i) {
-    const int e = i * SH::NT + static_cast<int>(threadIdx.x);
-    dkey[i] = e / SH::CPR;
-    dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
-  }
-  uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
-  auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
-    const int slot = t % kAttnRing;
-#pragma unroll
-    for (int i = 0; i < SH::LPT; ++i)
-      dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
-  };
-  // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
-  // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
-  auto dma = [&](int t, auto IC) {
-    constexpr int i = decltype(IC)::value;
-    const int e0 = i * SH::NT + wave * 64;
-    char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
-    // (passed as uint16_t*: a char* argument to this builtin makes clang
-    // drop the host launch stubs of later instantiations)
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
-    if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-    } else if (e0 < SH::CH) {
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-    }
-  };
-  auto issue_tile = [&](int t) {
-    read_roff(t, roff);
-    attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
-  };
+    const float sink_v = hvalid ? a.sink[hq] : 0.f;
 
-  // Ring protocol: tile t lives in slot t % 4 and its P^T in p_lds[t % 2].
-  // Iteration `it` computes P.V of tile it and S^T + softmax of tile it+1,
-  // and ends with the one barrier of the tile.  The copies of tile it+3 are
-  // issued from the start of the iteration into the slot of tile it-1 (which
-  // all waves finished in iteration it-1) and must land by the end of
-  // iteration it+1: two iterations of gather latency.  Wave 0 copies the raw
-  // indices of tile it+6 at the start and publishes those of tile it+5
-  // (copied one iteration earlier) before the barrier; the row offsets of tile it+4 and
-  // the key biases of tile it+2 are read one iteration ahead into registers,
-  // so an iteration starts its copies and its softmax without waiting for LDS.
+    // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
+    // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
+    // offset is a per-lane base (one per ks parity) plus 64 ks + 16 ROW mb.
+    const int qf_swz = kv_swz<D>(i16);
+    const int qbase = i16 * ROW + 16 * (g ^ (qf_swz & 3));
+    const int qadj = 64 * (qf_swz >> 2);
+    float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
+    float l_run = 0.f;       // this lane's share of the denominator
 
-  // ---- Q^T fragments and the sink --------------------------------------------
-  bf16x8 qf[KS];
-  {
-    const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
-  }
-  const float sink_v = hvalid ? a.sink[hq] : 0.f;
-
-  // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
-  // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
-  // offset is a per-lane base (one per ks parity) plus 64 ks + 16 ROW mb.
-  const int qf_swz = kv_swz<D>(i16);
-  const int qbase = i16 * ROW + 16 * (g ^ (qf_swz & 3));
-  const int qadj = 64 * (qf_swz >> 2);
-  // V^T transposing-read address: source lane (g, i16) points at key
-  // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
-  // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
-  // swizzles to 8j + (x ^ f), so block j is at a fixed base + 128 j.
-  const int tkey = 4 * g + (i16 >> 2);
-  const int tx = 2 * wave + ((i16 & 3) >> 1);
-  const int tbase = tkey * ROW + 16 * ((tx ^ kv_swz<D>(tkey)) & (SH::CPR - 1)) + 8 * (i16 & 1);
-
-  f32x4 oacc[MBW][4];
-#pragma unroll
-  for (int j = 0; j < MBW; ++j)
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
-  float l_run = 0.f;       // this lane's share of the denominator
-
-  // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
-  // A-fragments stream through a QPD-deep register queue: each MFMA's operand
-  // was read from LDS QPD k-steps earlier.  With ISSUE, the copies of tile
-  // t+1 are issued between the k-steps.
-  constexpr int QPD = KS < 4 ? KS : 4;
-  auto qk = [&](int t, f32x4 (&st)[2], auto ISSUE_C) {
-    constexpr bool ISSUE = decltype(ISSUE_C)::value;
-    const uint32_t tile = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE);
-    const uint32_t qa_e = tile + qbase + qadj;
-    const uint32_t qa_o = tile + qbase - qadj;
-    bf16x8 kq[QPD][2];
-    auto qk_issue = [&](auto KC) {
-      constexpr int ks = decltype(KC)::value;
-      const uint32_t base = (ks & 1) ? qa_o : qa_e;
-      kq[ks % QPD][0] = ld128<64 * ks>(base);
-      kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+    // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
+    // A-fragments stream through a QPD-deep register queue: each MFMA's
+    // operand was read from LDS QPD k-steps earlier.
+    constexpr int QPD = KS < 4 ? KS : 4;
+    auto qk = [&](int t, f32x4 (&st)[2]) {
+      const uint32_t tile = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE);
+      const uint32_t qa_e = tile + qbase + qadj;
+      const uint32_t qa_o = tile + qbase - qadj;
+      bf16x8 kq[QPD][2];
+      auto qk_issue = [&](auto KC) {
+        constexpr int ks = decltype(KC)::value;
+        const uint32_t base = (ks & 1) ? qa_o : qa_e;
+        kq[ks % QPD][0] = ld128<64 * ks>(base);
+        kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+      };
+      attn_static_for<0, QPD>(qk_issue);
+      st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto qk_step = [&](auto KC) {
+        constexpr int ks = decltype(KC)::value;
+        constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
+        lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
+        st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
+        st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
+        if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
+      };
+      attn_static_for<0, KS>(qk_step);
+      mfma_result_fence(st[0], st[1]);
     };
-    attn_static_for<0, QPD>(qk_issue);
-    st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto qk_step = [&](auto KC) {
-      constexpr int ks = decltype(KC)::value;
-      constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
-      lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
-      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
-      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
-      if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
-      if constexpr (ISSUE && ks % 2 == 0 && ks / 2 < SH::LPT) dma(t + 1, std::integral_constant<int, ks / 2>{});
-    };
-    attn_static_for<0, KS>(qk_step);
-    if constexpr (ISSUE && (KS + 1) / 2 < SH::LPT)
-      attn_static_for<(KS + 1) / 2, SH::LPT>([&](auto IC) { dma(t + 1, IC); });
-    mfma_result_fence(st[0], st[1]);
-  };
 
-  // Online softmax of tile t for head hq, in registers, as kSmStages steps
-  // of similar VALU length so that they can be interleaved with the MFMAs of
-  // the previous tile's P.V; the result (P^T as a bf16 B-fragment and the
-  // head's rescale factor) is published by softmax_store.
-  struct SoftmaxOut {
-    u32x4 w;
-    float alpha;
-  };
-  struct SmState {
-    float x[2][4];
-    float tmax;
-    f32x2 p[4];
-    SoftmaxOut out;
-  };
-  constexpr int kSmStages = 6;
-  auto sm_stage = [&](SmState& S, const f32x4 (&st)[2], const f32x4 (&bias)[2], auto SC) {
-    constexpr int k = decltype(SC)::value;
-    if constexpr (k == 0) {  // scaled scores, masked keys at -inf; tile maximum
+    // Online softmax of tile t for head hq, in registers; the result (P^T as
+    // a bf16 B-fragment and the head's rescale factor) is published by
+    // softmax_store.
+    struct SoftmaxOut {
+      u32x4 w;
+      float alpha;
+    };
+    auto softmax = [&](const f32x4 (&st)[2], const f32x4 (&bias)[2]) {
+      SoftmaxOut out;
+      float x[2][4];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S.x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
-      S.tmax = __builtin_fmaxf(
-          __builtin_fmaxf(__builtin_fmaxf(S.x[0][0], S.x[0][1]), __builtin_fmaxf(S.x[0][2], S.x[0][3])),
-          __builtin_fmaxf(__builtin_fmaxf(S.x[1][0], S.x[1][1]), __builtin_fmaxf(S.x[1][2], S.x[1][3])));
-    } else if constexpr (k == 1) {  // max over lane groups g ^ 1
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(S.tmax), __float_as_uint(S.tmax), false, false);
-      S.tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-    } else if constexpr (k == 2) {  // max over lane groups g ^ 2; move the reference
-      const SwapPair r32 = permlane32_swap(__float_as_uint(S.tmax), __float_as_uint(S.tmax));
-      const float tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+        for (int r = 0; r < 4; ++r) x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
+      // tile maximum: in-lane, then over the lane groups g ^ 1 and g ^ 2
+      float tmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0][0], x[0][1]), __builtin_fmaxf(x[0][2], x[0][3])),
+                                   __builtin_fmaxf(__builtin_fmaxf(x[1][0], x[1][1]), __builtin_fmaxf(x[1][2], x[1][3])));
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
+      tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
       // First valid key of the head: the accumulator and denominator are
       // still zero, so the reference moves without a rescale (alpha = 1).
       const bool first = m_ref == -1.0e30f;
       const bool raise = first ? tmax > m_ref : tmax > m_ref + kLazyRescale;
       const float m_new = raise ? tmax : m_ref;
-      S.out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
+      out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
       m_ref = m_new;
-    } else if constexpr (k == 3 || k == 4) {
-      constexpr int mb = k - 3;
-      S.p[2 * mb] = f32x2{__builtin_amdgcn_exp2f(S.x[mb][0] - m_ref), __builtin_amdgcn_exp2f(S.x[mb][1] - m_ref)};
-      S.p[2 * mb + 1] = f32x2{__builtin_amdgcn_exp2f(S.x[mb][2] - m_ref), __builtin_amdgcn_exp2f(S.x[mb][3] - m_ref)};
-    } else if constexpr (k == 5) {
-      const float psum = ((S.p[0][0] + S.p[0][1]) + (S.p[1][0] + S.p[1][1])) +
-                         ((S.p[2][0] + S.p[2][1]) + (S.p[3][0] + S.p[3][1]));
-      l_run = l_run * S.out.alpha + psum;
+      f32x2 p[4];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        p[2 * mb] = f32x2{__builtin_amdgcn_exp2f(x[mb][0] - m_ref), __builtin_amdgcn_exp2f(x[mb][1] - m_ref)};
+        p[2 * mb + 1] = f32x2{__builtin_amdgcn_exp2f(x[mb][2] - m_ref), __builtin_amdgcn_exp2f(x[mb][3] - m_ref)};
+      }
+      const float psum = ((p[0][0] + p[0][1]) + (p[1][0] + p[1][1])) + ((p[2][0] + p[2][1]) + (p[3][0] + p[3][1]));
+      l_run = l_run * out.alpha + psum;
       // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
 #pragma unroll
-      for (int c = 0; c < 4; ++c) S.out.w[c] = f32x2_to_bf16x2(S.p[c][0], S.p[c][1]);
-    }
-  };
-  auto softmax = [&](const f32x4 (&st)[2], const f32x4 (&bias)[2]) {
-    SmState S;
-    attn_static_for<0, kSmStages>([&](auto SC) { sm_stage(S, st, bias, SC); });
-    return S.out;
-  };
-  auto softmax_store = [&](int t, const SoftmaxOut& r) {
-    *reinterpret_cast<u32x4*>(&p_lds[t & 1][(wave * 64 + lane) * 16]) = r.w;
-    if (g == 0) alpha_lds[t & 1][wave * 16 + i16] = r.alpha;
-  };
-
-  // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r).
-  auto read_bias = [&](int t, f32x4 (&bias)[2]) {
-    bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
-    bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
-  };
-
-  // One pipelined iteration.  P.V of tile it (O^T += V^T P^T for this wave's
-  // 16-dim blocks, all 64 heads) runs alongside S^T of tile it+1 and then
-  // alongside the softmax of tile it+1, in one stream of MFMAs; the copies
-  // of tile it+3 are issued in between.  ISSUE: tile it+3 exists; NXT: tile
-  // it+1 exists; WAIT2: tile it+2 exists (its copies must land by the end).
-  f32x4 bias_cur[2], bias_nx[2];   // key biases of tiles it+1 and it+2
-  uint32_t roff_nx[SH::LPT];       // copy sources of tile it+4
-  constexpr int kPreCopies = SH::LPT < 3 ? SH::LPT : 3;  // copies issued before the MFMA stream
-  auto iteration = [&](int it, auto ISSUE_C, auto NXT_C, auto WAIT2_C) {
-    constexpr bool ISSUE = decltype(ISSUE_C)::value;
-    constexpr bool NXT = decltype(NXT_C)::value;
-    constexpr bool WAIT2 = decltype(WAIT2_C)::value;
-    using SC = AttnSched<KS, MBW, NXT>;
-    // ---- rescale factors of tile it (needed now); row offsets of tile it+4
-    // and key biases of tile it+2 (for the next iteration; the slots read are
-    // always inside the arrays, so the reads need no guard)
-    float al[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
-    read_roff(it + 4, roff_nx);
-    read_bias(it + 2, bias_nx);
-    if (wave == 0 && it + 6 < ntiles) load_idx(it + 6);
-    if constexpr (ISSUE) attn_static_for<0, kPreCopies>([&](auto IC) { dma(it + 3, IC); });
-    const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
-                                                         al[3] != 1.0f) != 0;
-    if (__builtin_expect(any_rescale, 0)) {
-#pragma unroll
-      for (int j = 0; j < MBW; ++j)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- pipelined LDS reads, in the order AttnSched describes
-    const uint32_t pa = lds_addr(&p_lds[it & 1][0]) + lane * 16;
-    bf16x8 pbr[4];
-    pbr[0] = ld128<0>(pa);
-    pbr[1] = ld128<1024>(pa);
-    pbr[2] = ld128<2048>(pa);
-    pbr[3] = ld128<3072>(pa);
-    const uint32_t ta = lds_addr(kv_lds + (it % kAttnRing) * SH::TILE) + tbase;
-    v4i16 lo[3], hi[3];
-    lo[0] = tr_read<0>(ta);
-    hi[0] = tr_read<16 * ROW>(ta);
-    if constexpr (MBW > 1) {
-      lo[1] = tr_read<128>(ta);
-      hi[1] = tr_read<16 * ROW + 128>(ta);
-    }
-    const uint32_t qtile = lds_addr(kv_lds + ((it + 1) % kAttnRing) * SH::TILE);
-    const uint32_t qa_e = qtile + qbase + qadj;
-    const uint32_t qa_o = qtile + qbase - qadj;
-    constexpr int QPD = SC::QPD;
-    bf16x8 kq[QPD][2];
-    auto kq_issue = [&](auto KC) {
-      constexpr int ks = decltype(KC)::value;
-      const uint32_t base = (ks & 1) ? qa_o : qa_e;
-      kq[ks % QPD][0] = ld128<64 * ks>(base);
-      kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+      for (int c = 0; c < 4; ++c) out.w[c] = f32x2_to_bf16x2(p[c][0], p[c][1]);
+      return out;
     };
-    if constexpr (NXT) attn_static_for<0, QPD>(kq_issue);
+    auto softmax_store = [&](int t, const SoftmaxOut& r) {
+      *reinterpret_cast<u32x4*>(&p_lds[t & 1][(wave * 64 + lane) * 16]) = r.w;
+      if (g == 0) alpha_lds[t & 1][wave * 16 + i16] = r.alpha;
+    };
+    // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r);
+    // the slot read is always inside the array, so no guard is needed.
+    auto read_bias = [&](int t, f32x4 (&bias)[2]) {
+      bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
+      bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
+    };
 
-    f32x4 st[2];
-    SmState S;
-    auto step = [&](auto UC) {
-      constexpr int u = decltype(UC)::value;
-      constexpr int w = SC::wait_at(u);
-      if constexpr (w >= 0) lds_wait_n<w>();
-      if constexpr (NXT && u < KS) {
-        reg_tie(kq[u % QPD][0]);
-        reg_tie(kq[u % QPD][1]);
-      }
-      if constexpr (u % 4 == 0) {
-        reg_tie(lo[(u / 4) % 3]);
-        reg_tie(hi[(u / 4) % 3]);
-      }
-      if constexpr (u == 0) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) reg_tie(pbr[nb]);
-      }
-      if constexpr (NXT && u < KS) {
-        const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
-        st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[u % QPD][0], qf[u], u == 0 ? z : st[0], 0, 0, 0);
-        st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[u % QPD][1], qf[u], u == 0 ? z : st[1], 0, 0, 0);
-      }
+    if (ntiles > 0) {
+      __syncthreads();  // indices of tiles 0..3 published
+      __syncthreads();  // tile 0 landed
+      f32x4 bias_cur[2];
       {
-        constexpr int j = u / 4, nb = u % 4;
-        const bf16x8 vf =
-            __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j % 3], hi[j % 3], 0, 1, 2, 3, 4, 5, 6, 7));
-        oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pbr[nb], oacc[j][nb], 0, 0, 0);
+        f32x4 bias[2], st[2];
+        read_bias(0, bias);
+        qk(0, st);
+        softmax_store(0, softmax(st, bias));
       }
-      if constexpr (SC::kq_at(u)) kq_issue(std::integral_constant<int, u + QPD>{});
-      if constexpr (SC::tr_at(u)) {
-        constexpr int j2 = u / 4 + 2;
-        lo[j2 % 3] = tr_read<128 * j2>(ta);
-        hi[j2 % 3] = tr_read<16 * ROW + 128 * j2>(ta);
+      read_bias(1, bias_cur);
+      __syncthreads();  // tile 1 landed; P^T of tile 0 published
+      __syncthreads();  // indices of tile 4 published
+      for (int it = 0; it < ntiles; ++it) {
+        if (it + 1 < ntiles) {
+          f32x4 bias_nx[2], st[2];
+          read_bias(it + 2, bias_nx);
+          qk(it + 1, st);
+          softmax_store(it + 1, softmax(st, bias_cur));
+          bias_cur[0] = bias_nx[0];
+          bias_cur[1] = bias_nx[1];
+        }
+        __syncthreads();
       }
-      if constexpr (ISSUE && u + kPreCopies < SH::LPT) dma(it + 3, std::integral_constant<int, u + kPreCopies>{});
-      if constexpr (NXT) {
-        attn_static_for<0, kSmStages>([&](auto KC) {
-          constexpr int k = decltype(KC)::value;
-          if constexpr (SC::sm_step(k, kSmStages) == u) sm_stage(S, st, bias_cur, KC);
-        });
+    }
+
+    // ---- denominators, sink, normalisation factor, lse ----------------------
+    float l_tot;
+    {  // sum over the four lane groups
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+      l_tot = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+      const SwapPair r32 = permlane32_swap(__float_as_uint(l_tot), __float_as_uint(l_tot));
+      l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
+    }
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
+    const float m_fin = __builtin_fmaxf(m_ref, sink2);
+    const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
+    const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
+    const float scale = l_fin > 0.f ? resc / l_fin : 0.f;
+    if (g == 0) {
+      scale_lds[wave * 16 + i16] = scale;
+      if (hvalid) {
+        constexpr float kLn2 = 0.6931471805599453f;
+        const float lse = l_fin > 0.f ? (__builtin_amdgcn_logf(l_fin) + m_fin) * kLn2 : -1.0e30f;
+        a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(hq) * a.lsh] = lse;
+      }
+    }
+    __syncthreads();  // normalisation factors published
+    __syncthreads();  // output staged
+  } else {
+    // ============== P.V, KV gather and the index pipeline =====================
+    const int ctid = static_cast<int>(threadIdx.x) - kAttnWaves * 64;  // 0 .. SH::NT-1
+    const bool idx_wave = wave == 0;
+    const char* idx_row = static_cast<const char*>(a.idx) +
+                          (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
+    const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+
+    // Key indices of tile `t`: the index wave copies the raw index words into
+    // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
+    // no loop-carried load result forces an early wait), and after its next
+    // full wait reads them back, validates them and publishes validity and
+    // row offsets to ring slot t % 4 for every wave.
+    auto load_idx = [&](int t) {
+      // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
+      int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
+      j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
+      const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
+                                       (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
+    };
+    auto store_idx = [&](int t) {
+      const int slot = t % kAttnRing;
+      const int rslot = t % (2 * kAttnRing);
+      if (lane < kAttnTK) {
+        const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
+                                                         idxraw_lds[rslot][2 * lane])
+                                  : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
+        const int j = t * kAttnTK + lane;
+        const bool ok = j < a.K && raw >= 0 && raw < a.N;
+        bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
+        rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
       }
     };
-    attn_static_for<0, SC::NSTEP>(step);
-    if constexpr (NXT) softmax_store(it + 1, S.out);
-    bias_cur[0] = bias_nx[0];
-    bias_cur[1] = bias_nx[1];
+    // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
+    // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
+    // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
+    // source is kv + 16 (rowoff16[key] + dcoff).
+    int dkey[SH::LPT], dcoff[SH::LPT];
 #pragma unroll
-    for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
-    // copies of tile it+2 and indices of tile it+5 (both issued one iteration
-    // ago) landed; the copies of tile it+3 and, in wave 0, the indices of
-    // tile it+6 may stay in flight
-    if constexpr (WAIT2 && ISSUE) {
-      if (wave == 0 && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT + 1));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-    } else {
-      __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+    for (int i = 0; i < SH::LPT; ++i) {
+      const int e = i * SH::NT + ctid;
+      dkey[i] = e / SH::CPR;
+      dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
     }
-    if (wave == 0 && it + 5 < ntiles) store_idx(it + 5);
-    __syncthreads();
-  };
+    uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
+    auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
+      const int slot = t % kAttnRing;
+#pragma unroll
+      for (int i = 0; i < SH::LPT; ++i)
+        dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+    };
+    // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
+    // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
+    auto dma = [&](int t, auto IC) {
+      constexpr int i = decltype(IC)::value;
+      const int e0 = i * SH::NT + wave * 64;
+      char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
+      // (passed as uint16_t*: a char* argument to this builtin makes clang
+      // drop the host launch stubs of later instantiations)
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+      if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+      } else if (e0 < SH::CH) {
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+      }
+    };
+    auto issue_tile = [&](int t) {
+      read_roff(t, roff);
+      attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
+    };
 
-  if (ntiles > 0) {
-    // indices of tiles 0..5; tile 4 shares its row-offset / bias slot with
-    // tile 0, so it is published once tile 0's entries have been read, and
-    // tile 5 at the end of iteration 0
-    if (wave == 0) {
-      const int np = ntiles < 6 ? ntiles : 6;
-      for (int t = 0; t < np; ++t) load_idx(t);
-      __builtin_amdgcn_s_waitcnt(0x7 << 4);
-      for (int t = 0; t < np && t < 4; ++t) store_idx(t);
-    }
-    __syncthreads();
-    issue_tile(0);
-    if (ntiles > 1) issue_tile(1);
-    if (ntiles > 2) issue_tile(2);
-    // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
-    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
-    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-    else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-    __syncthreads();
-    {
-      f32x4 bias[2];
-      read_bias(0, bias);
-      f32x4 st[2];
-      qk(0, st, std::false_type{});
-      softmax_store(0, softmax(st, bias));
-    }
-    read_bias(1, bias_cur);
-    read_roff(3, roff);
-    // tile 1 landed; the copies of tile 2 may still be in flight
-    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-    else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-    __syncthreads();  // also: every wave has read tile 0's row offsets and biases
-    if (wave == 0 && ntiles > 4) store_idx(4);
-    __syncthreads();
-    int it = 0;
-    for (; it + 3 < ntiles; ++it) iteration(it, std::true_type{}, std::true_type{}, std::true_type{});
-    if (it + 2 < ntiles) iteration(it++, std::false_type{}, std::true_type{}, std::true_type{});
-    if (it + 1 < ntiles) iteration(it++, std::false_type{}, std::true_type{}, std::false_type{});
-    iteration(it, std::false_type{}, std::false_type{}, std::false_type{});
-  }
+    // V^T transposing-read address: source lane (g, i16) points at key
+    // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
+    // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
+    // swizzles to 8j + (x ^ f), so block j is at a fixed base + 128 j.
+    const int tkey = 4 * g + (i16 >> 2);
+    const int tx = 2 * wave + ((i16 & 3) >> 1);
+    const int tbase = tkey * ROW + 16 * ((tx ^ kv_swz<D>(tkey)) & (SH::CPR - 1)) + 8 * (i16 & 1);
 
-  // ---- finish: denominators, sink, normalisation, lse ---------------------
-  float l_tot;
-  {  // sum over the four lane groups
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-    l_tot = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-    const SwapPair r32 = permlane32_swap(__float_as_uint(l_tot), __float_as_uint(l_tot));
-    l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
-  }
-  constexpr float kLog2e = 1.4426950408889634f;
-  const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
-  const float m_fin = __builtin_fmaxf(m_ref, sink2);
-  const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
-  const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
-  const float scale = l_fin > 0.f ? resc / l_fin : 0.f;
-  if (g == 0) {
-    scale_lds[wave * 16 + i16] = scale;
-    if (hvalid) {
-      constexpr float kLn2 = 0.6931471805599453f;
-      const float lse = l_fin > 0.f ? (__builtin_amdgcn_logf(l_fin) + m_fin) * kLn2 : -1.0e30f;
-      a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(hq) * a.lsh] = lse;
+    f32x4 oacc[MBW][4];
+#pragma unroll
+    for (int j = 0; j < MBW; ++j)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // O^T += V^T P^T of tile `it` for this wave's 16-dim blocks and all 64
+    // heads.  The P^T fragments and the V^T blocks are read from inline asm
+    // with exact waits: blocks j and j+1 are in flight while block j's MFMAs
+    // run (LDS operations complete in order, so waiting for "at most 2
+    // outstanding" covers everything issued before block j+1).
+    auto pv = [&](int it) {
+      const uint32_t pa = lds_addr(&p_lds[it & 1][0]) + lane * 16;
+      bf16x8 pbr[4];
+      pbr[0] = ld128<0>(pa);
+      pbr[1] = ld128<1024>(pa);
+      pbr[2] = ld128<2048>(pa);
+      pbr[3] = ld128<3072>(pa);
+      const uint32_t ta = lds_addr(kv_lds + (it % kAttnRing) * SH::TILE) + tbase;
+      v4i16 lo[2], hi[2];
+      lo[0] = tr_read<0>(ta);
+      hi[0] = tr_read<16 * ROW>(ta);
+      if constexpr (MBW > 1) {
+        lo[1] = tr_read<128>(ta);
+        hi[1] = tr_read<16 * ROW + 128>(ta);
+      }
+      auto block = [&](auto JC) {
+        constexpr int j = decltype(JC)::value;
+        if constexpr (j + 1 < MBW) lds_wait<2>(lo[j & 1], hi[j & 1]); else lds_wait<0>(lo[j & 1], hi[j & 1]);
+        if constexpr (j == 0) {
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) reg_tie(pbr[nb]);
+        }
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j & 1], hi[j & 1], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pbr[nb], oacc[j][nb], 0, 0, 0);
+        if constexpr (j + 2 < MBW) {
+          lo[j & 1] = tr_read<128 * (j + 2)>(ta);
+          hi[j & 1] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
+        }
+      };
+      attn_static_for<0, MBW>(block);
+    };
+
+    // One consumer iteration.  ISSUE: tile it+3 exists (its copies start now);
+    // WAIT2: tile it+2 exists (its copies, issued one iteration ago, must land).
+    uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
+    auto iteration = [&](int it, auto ISSUE_C, auto WAIT2_C) {
+      constexpr bool ISSUE = decltype(ISSUE_C)::value;
+      constexpr bool WAIT2 = decltype(WAIT2_C)::value;
+      float al[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+      read_roff(it + 4, roff_nx);  // the slot read is always inside the array
+      if (idx_wave && it + 6 < ntiles) load_idx(it + 6);
+      // The copies go out in one burst before any LDS read that the compiler
+      // tracks: it makes such a read wait for every LDS-DMA copy issued
+      // before it (vmcnt(0)), and the P.V reads below are inline asm.
+      if constexpr (ISSUE) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
+      const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
+                                                           al[3] != 1.0f) != 0;
+      if (__builtin_expect(any_rescale, 0)) {
+#pragma unroll
+        for (int j = 0; j < MBW; ++j)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
+      }
+      pv(it);
+#pragma unroll
+      for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
+      // copies of tile it+2 and indices of tile it+5 (both issued one
+      // iteration ago) landed; the copies of tile it+3 and, in the index
+      // wave, the indices of tile it+6 may stay in flight
+      if constexpr (WAIT2 && ISSUE) {
+        if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT + 1));
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      } else {
+        __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+      }
+      if (idx_wave && it + 5 < ntiles) store_idx(it + 5);
+    };
+
+    if (ntiles > 0) {
+      // indices of tiles 0..5; tile 4 shares its row-offset / bias slot with
+      // tile 0, so it is published once tile 0's entries have been read, and
+      // tile 5 at the end of iteration 0
+      if (idx_wave) {
+        const int np = ntiles < 6 ? ntiles : 6;
+        for (int t = 0; t < np; ++t) load_idx(t);
+        __builtin_amdgcn_s_waitcnt(0x7 << 4);
+        for (int t = 0; t < np && t < 4; ++t) store_idx(t);
+      }
+      __syncthreads();  // indices of tiles 0..3 published
+      issue_tile(0);
+      if (ntiles > 1) issue_tile(1);
+      if (ntiles > 2) issue_tile(2);
+      // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
+      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
+      else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+      __syncthreads();  // tile 0 landed
+      read_roff(3, roff);
+      // tile 1 landed; the copies of tile 2 may still be in flight
+      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+      __syncthreads();  // tile 1 landed; every wave has read tile 0's row offsets and biases
+      if (idx_wave && ntiles > 4) store_idx(4);
+      __syncthreads();  // indices of tile 4 published
+      int it = 0;
+      for (; it + 3 < ntiles; ++it) {
+        iteration(it, std::true_type{}, std::true_type{});
+        __syncthreads();
+      }
+      if (it + 2 < ntiles) {
+        iteration(it++, std::false_type{}, std::true_type{});
+        __syncthreads();
+      }
+      if (it + 1 < ntiles) {
+        iteration(it++, std::false_type{}, std::false_type{});
+        __syncthreads();
+      }
+      iteration(it, std::false_type{}, std::false_type{});
+      __syncthreads();
     }
-  }
-  __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
-  __syncthreads();
-  // Normalised O (bf16) staged head-major in LDS: [64 heads][OROW bytes].
-  float sc[4];
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
+    __syncthreads();  // normalisation factors published
+    // Normalised O (bf16) staged head-major in LDS: [64 heads][OROW bytes].
+    float sc[4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) sc[nb] = scale_lds[nb * 16 + i16];
+    for (int nb = 0; nb < 4; ++nb) sc[nb] = scale_lds[nb * 16 + i16];
 #pragma unroll
-  for (int j = 0; j < MBW; ++j) {
-    const int mbi = j * kAttnWaves + wave;
-    if (SH::MBT % kAttnWaves == 0 || mbi < SH::MBT) {
+    for (int j = 0; j < MBW; ++j) {
+      const int mbi = j * kAttnWaves + wave;
+      if (SH::MBT % kAttnWaves == 0 || mbi < SH::MBT) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        uint2 w;
-        w.x = f32x2_to_bf16x2(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
-        w.y = f32x2_to_bf16x2(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
-        *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
+        for (int nb = 0; nb < 4; ++nb) {
+          uint2 w;
+          w.x = f32x2_to_bf16x2(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
+          w.y = f32x2_to_bf16x2(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
+          *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
+        }
       }
     }
+    __syncthreads();  // output staged
   }
-  __syncthreads();
+
+  // ---- coalesced 16-byte stores of the staged output (all threads) ---------
   const int hcount = (a.H - hbase) < 64 ? (a.H - hbase) : 64;
   uint16_t* obase = a.o + b * a.osb + static_cast<int64_t>(s) * a.oss + static_cast<int64_t>(hbase) * a.osh;
-  for (int e = threadIdx.x; e < hcount * SH::CPR; e += SH::NT) {
+  for (int e = threadIdx.x; e < hcount * SH::CPR; e += kAttnThreads) {
     const int h = e / SH::CPR, c = e % SH::CPR;
     *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(h) * a.osh + c * 8) =
         *reinterpret_cast<const u32x4*>(kv_lds + h * SH::OROW + c * 16);
@@ -685,10 +628,10 @@ static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
   const int64_t nblk = static_cast<int64_t>(a.B) * a.S * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
   if (a.idx64) {
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64),
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnThreads),
                        0, st, a);
   } else {
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnWaves * 64),
+    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnThreads),
                        0, st, a);
   }
   return check_launch("sparse_attn_fwd_kernel");
