@@ -188,6 +188,20 @@ __device__ __forceinline__ void reg_tie(T& x) {
   asm volatile("" : "+v"(x));
 }
 
+// Tile barrier of the main loops.  __syncthreads() carries a workgroup
+// release fence, for which the compiler waits on every outstanding LDS-DMA
+// copy (vmcnt(0)) -- including the gathers just issued for later tiles, which
+// would leave no gather latency hidden.  Here each wave first waits for
+// exactly what the other waves read after the barrier (its LDS stores:
+// lgkmcnt(0); the copies of the next tile: an explicit vmcnt), and the empty
+// asm statements keep the compiler from moving memory accesses across the
+// barrier.
+__device__ __forceinline__ void attn_tile_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Threads of a workgroup: kAttnWaves S^T / softmax waves ("producers", 16
 // heads each) and kAttnWaves P.V waves ("consumers", 16-dim output blocks
 // dealt round-robin), one of each per SIMD.
@@ -254,6 +268,48 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
     const int qadj = 64 * (qf_swz >> 2);
     float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
     float l_run = 0.f;       // this lane's share of the denominator
+
+    // ---- KV gather (issued by the producers, which wait at the tile barrier
+    // for the P.V waves otherwise) -------------------------------------------
+    const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+    // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
+    // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
+    // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
+    // source is kv + 16 (rowoff16[key] + dcoff).
+    int dkey[SH::LPT], dcoff[SH::LPT];
+#pragma unroll
+    for (int i = 0; i < SH::LPT; ++i) {
+      const int e = i * SH::NT + static_cast<int>(threadIdx.x);
+      dkey[i] = e / SH::CPR;
+      dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
+    }
+    uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
+    auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
+      const int slot = t % kAttnRing;
+#pragma unroll
+      for (int i = 0; i < SH::LPT; ++i)
+        dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+    };
+    // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
+    // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
+    auto dma = [&](int t, auto IC) {
+      constexpr int i = decltype(IC)::value;
+      const int e0 = i * SH::NT + wave * 64;
+      char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
+      // (passed as uint16_t*: a char* argument to this builtin makes clang
+      // drop the host launch stubs of later instantiations)
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+      if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+      } else if (e0 < SH::CH) {
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+      }
+    };
+    auto issue_tile = [&](int t) {
+      read_roff(t, roff);
+      attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
+    };
+
 
     // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
     // A-fragments stream through a QPD-deep register queue: each MFMA's
@@ -326,9 +382,16 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       for (int c = 0; c < 4; ++c) out.w[c] = f32x2_to_bf16x2(p[c][0], p[c][1]);
       return out;
     };
+    // (inline asm: the compiler makes a tracked LDS access that follows
+    // LDS-DMA copies wait for all of them; the tile barrier's lgkmcnt(0)
+    // orders these stores)
     auto softmax_store = [&](int t, const SoftmaxOut& r) {
-      *reinterpret_cast<u32x4*>(&p_lds[t & 1][(wave * 64 + lane) * 16]) = r.w;
-      if (g == 0) alpha_lds[t & 1][wave * 16 + i16] = r.alpha;
+      const uint32_t pa = lds_addr(&p_lds[t & 1][(wave * 64 + lane) * 16]);
+      asm volatile("ds_write_b128 %0, %1" ::"v"(pa), "v"(r.w) : "memory");
+      if (g == 0) {
+        const uint32_t aa = lds_addr(reinterpret_cast<const char*>(&alpha_lds[t & 1][wave * 16 + i16]));
+        asm volatile("ds_write_b32 %0, %1" ::"v"(aa), "v"(r.alpha) : "memory");
+      }
     };
     // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r);
     // the slot read is always inside the array, so no guard is needed.
@@ -339,27 +402,51 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
 
     if (ntiles > 0) {
       __syncthreads();  // indices of tiles 0..3 published
+      issue_tile(0);
+      if (ntiles > 1) issue_tile(1);
+      if (ntiles > 2) issue_tile(2);
+      // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
+      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
+      else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
       __syncthreads();  // tile 0 landed
       f32x4 bias_cur[2];
       {
         f32x4 bias[2], st[2];
         read_bias(0, bias);
+        read_bias(1, bias_cur);
+        read_roff(3, roff);
         qk(0, st);
         softmax_store(0, softmax(st, bias));
       }
-      read_bias(1, bias_cur);
-      __syncthreads();  // tile 1 landed; P^T of tile 0 published
+      // tile 1 landed; the copies of tile 2 may still be in flight
+      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+      __syncthreads();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
       __syncthreads();  // indices of tile 4 published
+      uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
       for (int it = 0; it < ntiles; ++it) {
+        const bool issue = it + 3 < ntiles;
+        // tracked LDS reads first, then the copies of tile it+3 into the slot
+        // of tile it-1 (finished by every wave in iteration it-1)
+        f32x4 bias_nx[2];
+        read_bias(it + 2, bias_nx);    // slots read are always inside the arrays
+        read_roff(it + 4, roff_nx);
+        if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
         if (it + 1 < ntiles) {
-          f32x4 bias_nx[2], st[2];
-          read_bias(it + 2, bias_nx);
+          f32x4 st[2];
           qk(it + 1, st);
           softmax_store(it + 1, softmax(st, bias_cur));
-          bias_cur[0] = bias_nx[0];
-          bias_cur[1] = bias_nx[1];
         }
-        __syncthreads();
+        bias_cur[0] = bias_nx[0];
+        bias_cur[1] = bias_nx[1];
+#pragma unroll
+        for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
+        // the copies of tile it+2 (issued one iteration ago) landed; those of
+        // tile it+3 stay in flight across the barrier
+        if (issue) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+        attn_tile_barrier();
       }
     }
 
@@ -389,11 +476,9 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
     __syncthreads();  // output staged
   } else {
     // ============== P.V, KV gather and the index pipeline =====================
-    const int ctid = static_cast<int>(threadIdx.x) - kAttnWaves * 64;  // 0 .. SH::NT-1
     const bool idx_wave = wave == 0;
     const char* idx_row = static_cast<const char*>(a.idx) +
                           (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
-    const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
 
     // Key indices of tile `t`: the index wave copies the raw index words into
     // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
@@ -421,44 +506,6 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
       }
     };
-    // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
-    // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
-    // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
-    // source is kv + 16 (rowoff16[key] + dcoff).
-    int dkey[SH::LPT], dcoff[SH::LPT];
-#pragma unroll
-    for (int i = 0; i < SH::LPT; ++i) {
-      const int e = i * SH::NT + ctid;
-      dkey[i] = e / SH::CPR;
-      dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
-    }
-    uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
-    auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
-      const int slot = t % kAttnRing;
-#pragma unroll
-      for (int i = 0; i < SH::LPT; ++i)
-        dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
-    };
-    // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
-    // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
-    auto dma = [&](int t, auto IC) {
-      constexpr int i = decltype(IC)::value;
-      const int e0 = i * SH::NT + wave * 64;
-      char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
-      // (passed as uint16_t*: a char* argument to this builtin makes clang
-      // drop the host launch stubs of later instantiations)
-      const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
-      if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-      } else if (e0 < SH::CH) {
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-      }
-    };
-    auto issue_tile = [&](int t) {
-      read_roff(t, roff);
-      attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
-    };
-
     // V^T transposing-read address: source lane (g, i16) points at key
     // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
     // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
@@ -511,21 +558,12 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       attn_static_for<0, MBW>(block);
     };
 
-    // One consumer iteration.  ISSUE: tile it+3 exists (its copies start now);
-    // WAIT2: tile it+2 exists (its copies, issued one iteration ago, must land).
-    uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
-    auto iteration = [&](int it, auto ISSUE_C, auto WAIT2_C) {
-      constexpr bool ISSUE = decltype(ISSUE_C)::value;
-      constexpr bool WAIT2 = decltype(WAIT2_C)::value;
+    // One consumer iteration: P.V of tile it and the index pipeline.
+    auto iteration = [&](int it) {
       float al[4];
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
-      read_roff(it + 4, roff_nx);  // the slot read is always inside the array
       if (idx_wave && it + 6 < ntiles) load_idx(it + 6);
-      // The copies go out in one burst before any LDS read that the compiler
-      // tracks: it makes such a read wait for every LDS-DMA copy issued
-      // before it (vmcnt(0)), and the P.V reads below are inline asm.
-      if constexpr (ISSUE) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
       const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
                                                            al[3] != 1.0f) != 0;
       if (__builtin_expect(any_rescale, 0)) {
@@ -535,17 +573,10 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
           for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
       }
       pv(it);
-#pragma unroll
-      for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
-      // copies of tile it+2 and indices of tile it+5 (both issued one
-      // iteration ago) landed; the copies of tile it+3 and, in the index
-      // wave, the indices of tile it+6 may stay in flight
-      if constexpr (WAIT2 && ISSUE) {
-        if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT + 1));
-        else __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      } else {
-        __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-      }
+      // the indices of tile it+5 (copied one iteration ago) landed; in the
+      // index wave those of tile it+6 may stay in flight
+      if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(1));
+      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
       if (idx_wave && it + 5 < ntiles) store_idx(it + 5);
     };
 
@@ -560,36 +591,14 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         for (int t = 0; t < np && t < 4; ++t) store_idx(t);
       }
       __syncthreads();  // indices of tiles 0..3 published
-      issue_tile(0);
-      if (ntiles > 1) issue_tile(1);
-      if (ntiles > 2) issue_tile(2);
-      // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
-      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
-      else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
       __syncthreads();  // tile 0 landed
-      read_roff(3, roff);
-      // tile 1 landed; the copies of tile 2 may still be in flight
-      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
       __syncthreads();  // tile 1 landed; every wave has read tile 0's row offsets and biases
       if (idx_wave && ntiles > 4) store_idx(4);
       __syncthreads();  // indices of tile 4 published
-      int it = 0;
-      for (; it + 3 < ntiles; ++it) {
-        iteration(it, std::true_type{}, std::true_type{});
-        __syncthreads();
+      for (int it = 0; it < ntiles; ++it) {
+        iteration(it);
+        attn_tile_barrier();  // (store_idx's LDS stores complete first)
       }
-      if (it + 2 < ntiles) {
-        iteration(it++, std::false_type{}, std::true_type{});
-        __syncthreads();
-      }
-      if (it + 1 < ntiles) {
-        iteration(it++, std::false_type{}, std::false_type{});
-        __syncthreads();
-      }
-      iteration(it, std::false_type{}, std::false_type{});
-      __syncthreads();
     }
     __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
     __syncthreads();  // normalisation factors published
