@@ -134,6 +134,39 @@ int si_csa_scores_topk(const float* scores, const int64_t* score_strides, int64_
 int si_hca_topk_idxs(int64_t B, int64_t S, int64_t n_win, int64_t n_compressed, int64_t m_prime,
                      int64_t idx_offset, int32_t* out_idx, const int64_t* out_strides, void* stream);
 
+/*
+ * Workspace of si_sparse_attn_bwd: the bytes needed to process the query
+ * rows in the fewest chunks that fit max_bytes (one chunk when the whole
+ * problem fits), or, when even one row does not fit, the one-row need.
+ * Returns -1 on bad arguments (si_last_error() says why).
+ */
+int64_t si_sparse_attn_bwd_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K,
+                                           int64_t max_bytes);
+
+/*
+ * Sparse-attention backward from the forward's saved o and lse.
+ * Replaces flash_sparse/triton/sparse_attn_bwd.py:286-416 (sparse_attn_bwd:
+ * _delta_kernel + _sparse_attn_bwd_kernel) and is what the autograd wrapper
+ * flash_sparse/triton/__init__.py:37-44 calls.
+ *
+ *   q, kv, attn_sink, topk_idxs, B..K, softmax_scale: as si_sparse_attn_fwd.
+ *   o [B,S,H,D] bf16, lse [B,S,H] fp32: the forward's outputs; dout: dL/do.
+ *   dq [B,S,H,D] bf16 (written), dkv [B,N_kv,D] bf16 (written; rows no query
+ *   selects are 0), dsink [H] fp32 (written).
+ *   workspace: at least si_sparse_attn_bwd_workspace_bytes(..., workspace_bytes)
+ *   bytes, 16-byte aligned; the rows are processed in chunks that fit it.
+ * dkv is reduced key by key in a fixed order (no atomics): repeated calls
+ * give identical results.  Supported: H <= 128, D in {32,64,128,256,512,576},
+ * B*S < 2^31, B*N_kv < 2^31.
+ */
+int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                       const float* attn_sink, const void* topk_idxs, int idx_is_i64, const int64_t* idx_strides,
+                       const void* o, const int64_t* o_strides, const float* lse, const int64_t* lse_strides,
+                       const void* dout, const int64_t* do_strides, int64_t B, int64_t S, int64_t H, int64_t D,
+                       int64_t N_kv, int64_t K, float softmax_scale, void* dq, const int64_t* dq_strides, void* dkv,
+                       const int64_t* dkv_strides, float* dsink, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

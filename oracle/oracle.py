@@ -23,6 +23,8 @@ Reference semantics followed (file:line in the reference tree):
 * set-overlap recall: ``eval/test_v4_indexer_parity.py:164-199``;
 * sparse attention with sink: ``flash_sparse/reference.py:44-130``;
   LSE: ``flash_sparse/triton/sparse_attn_fwd.py:148-177``;
+* sparse-attention backward from the saved (o, lse):
+  ``flash_sparse/triton/sparse_attn_bwd.py:1-26,93-97,224-283``;
 * CSA / HCA attention index rows: ``flash_sparse/csa.py:30-83,176-179``,
   ``flash_sparse/hca.py:24-51``, window ``flash_sparse/reference.py:460-475``.
 
@@ -70,6 +72,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_topk.argtypes = [P, I, I, P, P, I, P, P]
         L.oracle_topk.restype = None
         L.oracle_sparse_attn.argtypes = [P, P, P, P, I, I, I, I, I, ctypes.c_double, P, P]
+        L.oracle_sparse_attn_bwd.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, ctypes.c_double, P, I, P, P, P]
         L.oracle_sparse_attn.restype = None
         _lib = L
     return _lib
@@ -188,6 +191,40 @@ def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, 
     return o, lse
 
 
+def sparse_attn_bwd_rows(q_bits, kv_bits, o_bits, do_bits, sink, lse, idx, scale: float, *, want_dq: bool = True,
+                         keys: Optional[np.ndarray] = None, want_dkv: bool = True):
+    """Reference sparse-attention backward for ``n`` rows of one batch.
+
+    q_bits, o_bits, do_bits [n,H,D] uint16; kv_bits [N,D] uint16; sink [H] f32;
+    lse [n,H] f32; idx [n,K] int.  Returns (dq [n,H,D] or None, dkv, dsink [H]),
+    all float64.  dkv is [N,D] over every key, or [len(keys),D] for the listed
+    keys only (the contributions of these ``n`` rows; a sampled check passes
+    every row that selects a listed key).  dsink sums over the ``n`` rows.
+    """
+    n, H, D = q_bits.shape
+    N = kv_bits.shape[0]
+    K = idx.shape[1]
+    arrs = [np.ascontiguousarray(x, dtype=np.uint16) for x in (q_bits, kv_bits, o_bits, do_bits)]
+    sink = np.ascontiguousarray(sink, dtype=np.float32)
+    lse = np.ascontiguousarray(lse, dtype=np.float32)
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    dq = np.empty((n, H, D), dtype=np.float64) if want_dq else None
+    key_slot = None
+    nslot = N
+    if keys is not None:
+        keys = np.asarray(keys, dtype=np.int64)
+        key_slot = np.full(N, -1, dtype=np.int64)
+        key_slot[keys] = np.arange(len(keys))
+        nslot = len(keys)
+    dkv = np.zeros((nslot, D), dtype=np.float64) if want_dkv else None
+    dsink = np.zeros(H, dtype=np.float64)
+    lib().oracle_sparse_attn_bwd(_ptr(arrs[0]), _ptr(arrs[1]), _ptr(arrs[2]), _ptr(arrs[3]), _ptr(sink), _ptr(lse),
+                                 _ptr(idx), n, H, D, N, K, float(scale),
+                                 None if key_slot is None else _ptr(key_slot), nslot if want_dkv else 0,
+                                 None if dq is None else _ptr(dq), None if dkv is None else _ptr(dkv), _ptr(dsink))
+    return dq, dkv, dsink
+
+
 # ---------------------------------------------------------------------------
 # numpy restatements (tiny shapes only; cross-checks of the C oracle)
 # ---------------------------------------------------------------------------
@@ -245,7 +282,7 @@ def np_chunked_topk(scores: np.ndarray, lim: np.ndarray, top_k: int, chunk_t: in
 def np_sparse_attn(qf: np.ndarray, kvf: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float):
     """qf [n,H,D], kvf [N,D], sink [H], idx [n,K] -> (o [n,H,D], lse [n,H]); reference.py:93-130."""
     n, H, D = qf.shape
-    valid = idx >= 0
+    valid = (idx >= 0) & (idx < kvf.shape[0])                     # out of range: masked, as -1
     g = kvf[np.where(valid, idx, 0)] * valid[..., None]           # [n,K,D]
     sc = np.einsum("nhd,nkd->nhk", qf, g) * scale
     sc = np.where(valid[:, None, :], sc, -np.inf)
@@ -255,6 +292,30 @@ def np_sparse_attn(qf: np.ndarray, kvf: np.ndarray, sink: np.ndarray, idx: np.nd
     o = np.einsum("nhk,nkd->nhd", p, g) / den[..., None]
     lse = np.log(den) + mx
     return o, lse
+
+
+def np_sparse_attn_bwd(qf, kvf, of, dof, sink, lse, idx, scale: float):
+    """Backward of np_sparse_attn from its saved (o, lse), as
+    sparse_attn_bwd.py:1-26 states it: p = e^{scale q.k - lse},
+    ds = p (do.k - sum_d o do) scale, dq = sum_j ds k_j,
+    dkv[idx_j] += ds q + p do, dsink = -sum_rows e^{sink - lse} (o.do).
+    All float64; returns (dq [n,H,D], dkv [N,D], dsink [H])."""
+    n, H, D = qf.shape
+    N = kvf.shape[0]
+    valid = (idx >= 0) & (idx < N)
+    safe = np.where(valid, idx, 0)
+    g = kvf[safe] * valid[..., None]                                  # [n,K,D]
+    z = np.einsum("nhd,nkd->nhk", qf, g) * scale
+    p = np.where(valid[:, None, :], np.exp(z - lse[..., None]), 0.0)  # [n,H,K]
+    delta = (of * dof).sum(-1)                                        # [n,H]
+    dp = np.einsum("nhd,nkd->nhk", dof, g)
+    ds = p * (dp - delta[..., None]) * scale
+    dq = np.einsum("nhk,nkd->nhd", ds, g)
+    contrib = np.einsum("nhk,nhd->nkd", ds, qf) + np.einsum("nhk,nhd->nkd", p, dof)
+    dkv = np.zeros((N, D))
+    np.add.at(dkv, safe[valid], contrib[valid])
+    dsink = -(np.exp(sink[None, :] - lse) * delta).sum(0)
+    return dq, dkv, dsink
 
 
 # ---------------------------------------------------------------------------

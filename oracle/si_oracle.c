@@ -11,6 +11,7 @@
  *   tie order  docs/streaming_topk.md:46-60,301-312 (score desc, index asc)
  *   attention  flash_sparse/reference.py:44-130 (gather, sink-augmented softmax)
  *              flash_sparse/triton/sparse_attn_fwd.py:148-177 (LSE, -1e30 when empty)
+ *   backward   flash_sparse/triton/sparse_attn_bwd.py:1-26,93-97,224-283 (from saved o, lse)
  *
  * Arithmetic: bf16 inputs are widened exactly; every dot product and every
  * head/key sum is accumulated in double, which is at least as accurate as the
@@ -241,5 +242,89 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
     }
     free(sc);
     free(qd);
+  }
+}
+
+/*
+ * Sparse-attention backward for `nrows` query rows of one batch, from the
+ * forward's saved outputs, as the reference backward consumes them:
+ *   maths      flash_sparse/triton/sparse_attn_bwd.py:1-26
+ *   delta      sparse_attn_bwd.py:93-97   (sum_d o*do in fp32 from bf16 o, do)
+ *   gradients  sparse_attn_bwd.py:247-283 (p = exp(s - lse), dp = p (do.v - delta) scale,
+ *              dq = dp.kv, dkv[idx] += dp^T q + p^T do)
+ *   dsink      sparse_attn_bwd.py:224-228 (-exp(sink - lse) delta, summed over rows)
+ *   q, o, dout [nrows,H,D] bf16 bits; kv [N,D] bf16 bits; sink [H] fp32;
+ *   lse [nrows,H] fp32; idx [nrows,K] int64 (-1 or out of range = masked).
+ * Outputs, each optional (NULL = not wanted):
+ *   dq    [nrows,H,D]  written;
+ *   dkv   [nslot,D]    ACCUMULATED for keys t with key_slot[t] >= 0 into row
+ *                      key_slot[t] (key_slot NULL: slot t, nslot = N);
+ *   dsink [H]          ACCUMULATED (-sum_rows e^{sink-lse} delta).
+ * A key listed twice in a row contributes twice, as the reference's
+ * per-slot atomic adds do.  All sums in double.
+ */
+void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_t* o, const uint16_t* dout,
+                            const float* sink, const float* lse, const int64_t* idx, int64_t nrows, int64_t H,
+                            int64_t D, int64_t N, int64_t K, double scale, const int64_t* key_slot, int64_t nslot,
+                            double* dq, double* dkv, double* dsink) {
+  const int pairs = dq != NULL || (dkv != NULL && nslot > 0);
+#pragma omp parallel
+  {
+    double* qd = (double*)malloc(sizeof(double) * (size_t)D);
+    double* gd = (double*)malloc(sizeof(double) * (size_t)D);
+    double* kd = (double*)malloc(sizeof(double) * (size_t)D);
+    double* my_dkv = dkv ? (double*)calloc((size_t)(nslot > 0 ? nslot : 1) * (size_t)D, sizeof(double)) : NULL;
+    double* my_ds = (double*)calloc((size_t)H, sizeof(double));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t r = 0; r < nrows; ++r) {
+      const int64_t* ir = idx + r * K;
+      for (int64_t h = 0; h < H; ++h) {
+        const int64_t rh = r * H + h;
+        const double l = (double)lse[rh];
+        double delta = 0.0;
+        for (int64_t d = 0; d < D; ++d)
+          delta += (double)bf16_to_f32(o[rh * D + d]) * (double)bf16_to_f32(dout[rh * D + d]);
+        my_ds[h] -= exp((double)sink[h] - l) * delta;
+        if (!pairs) continue;
+        for (int64_t d = 0; d < D; ++d) {
+          qd[d] = (double)bf16_to_f32(q[rh * D + d]);
+          gd[d] = (double)bf16_to_f32(dout[rh * D + d]);
+        }
+        double* dqh = dq ? dq + rh * D : NULL;
+        if (dqh) for (int64_t d = 0; d < D; ++d) dqh[d] = 0.0;
+        for (int64_t j = 0; j < K; ++j) {
+          const int64_t t = ir[j];
+          if (t < 0 || t >= N) continue;
+          const int64_t slot = key_slot ? key_slot[t] : t;
+          if (!dqh && slot < 0) continue;
+          const uint16_t* kr = kv + t * D;
+          double qk = 0.0, gk = 0.0;
+          for (int64_t d = 0; d < D; ++d) {
+            kd[d] = (double)bf16_to_f32(kr[d]);
+            qk += qd[d] * kd[d];
+            gk += gd[d] * kd[d];
+          }
+          const double p = exp(scale * qk - l);
+          const double ds = p * (gk - delta) * scale; /* d loss / d (q.k) */
+          if (dqh) for (int64_t d = 0; d < D; ++d) dqh[d] += ds * kd[d];
+          if (my_dkv && slot >= 0) {
+            double* acc = my_dkv + slot * D;
+            for (int64_t d = 0; d < D; ++d) acc[d] += ds * qd[d] + p * gd[d];
+          }
+        }
+      }
+    }
+#pragma omp critical
+    {
+      if (dkv)
+        for (int64_t e = 0; e < nslot * D; ++e) dkv[e] += my_dkv[e];
+      if (dsink)
+        for (int64_t h = 0; h < H; ++h) dsink[h] += my_ds[h];
+    }
+    free(qd);
+    free(gd);
+    free(kd);
+    free(my_dkv);
+    free(my_ds);
   }
 }

@@ -5,7 +5,8 @@ Operators (hand-written HIP kernels behind the C ABI in
 
 * :func:`chunked_indexer_topk` — fused lightning-indexer score + exact top-k;
 * :func:`indexer_score`, :func:`indexer_score_topk`;
-* :func:`sparse_attn_fwd`, :func:`sparse_attn` — MQA sparse attention with sink;
+* :func:`sparse_attn_fwd`, :func:`sparse_attn_bwd`, :func:`sparse_attn` — MQA sparse attention
+  with sink, its backward and the autograd wrapper;
 * :func:`flash_csa_forward`, :func:`build_csa_topk_idxs`, :func:`csa_topk_idxs` —
   the CSA composition (fused indexer → window + compressed index rows → attention);
 * :func:`flash_hca_forward`, :func:`build_hca_topk_idxs` — HCA (window + every
@@ -16,7 +17,7 @@ The same names are importable under the reference's module paths through the
 """
 
 from .indexer import chunked_indexer_topk, indexer_score, indexer_score_topk
-from .sparse_attn import sparse_attn, sparse_attn_fwd
+from .sparse_attn import sparse_attn, sparse_attn_bwd, sparse_attn_fwd
 from .csa import build_csa_topk_idxs, csa_topk_idxs, flash_csa_forward
 from .hca import build_hca_topk_idxs, flash_hca_forward
 
@@ -27,6 +28,7 @@ __all__ = [
     "indexer_score",
     "indexer_score_topk",
     "sparse_attn",
+    "sparse_attn_bwd",
     "sparse_attn_fwd",
     "flash_csa_forward",
     "build_csa_topk_idxs",

@@ -40,6 +40,7 @@
 #include <string>
 #include <type_traits>
 
+#include "attn_common.h"
 #include "si_common.h"
 #include "si_status.h"
 
@@ -63,144 +64,11 @@ struct SparseAttnArgs {
   float scale_log2;    // softmax_scale * log2(e)
 };
 
-constexpr int kAttnTK = 32;      // keys per tile
-constexpr int kAttnWaves = 4;    // waves per workgroup; 16 heads each in S^T
-constexpr int kAttnRing = 4;     // KV tiles resident in LDS
 // The reference maximum of a head moves only when a tile's maximum exceeds it
 // by 2^64 (log2 units): p = 2^(x - m_ref) then stays below 2^64, far inside
 // the fp32/bf16 exponent range, and the output accumulator is rescaled only
 // on such a jump.  (Up to rounding the result equals the eager rescale.)
 constexpr float kLazyRescale = 64.0f;
-
-template <int D>
-struct AttnShape {
-  static constexpr int CPR = D / 8;                  // 16-byte chunks per KV row
-  static constexpr int ROW = D * 2;                  // bytes per KV row
-  static constexpr int TILE = kAttnTK * ROW;         // bytes per KV tile
-  static constexpr int CH = kAttnTK * CPR;           // chunks per tile
-  static constexpr int NT = kAttnWaves * 64;
-  static constexpr int LPT = (CH + NT - 1) / NT;     // tile copies per thread
-  static constexpr int KS = D / 32;                  // S^T k-steps
-  static constexpr int MBT = D / 16;                 // 16-dim output blocks
-  static constexpr int MBW = (MBT + kAttnWaves - 1) / kAttnWaves;  // per wave
-  static constexpr int OROW = ROW + 16;              // staged output row (padded)
-  static constexpr int OUT = 64 * OROW;              // staged output bytes
-  static constexpr int LDS_KV = (kAttnRing * TILE > OUT) ? kAttnRing * TILE : OUT;
-  static constexpr int FMASK = CPR >= 8 ? 7 : 0;     // chunk swizzle width
-};
-
-// Chunk swizzle of key row k: chunk c is stored at c ^ (k & 7).  Measured on
-// gfx950 (SQ_LDS_BANK_CONFLICT), this makes both read patterns below
-// conflict-free: the S^T A-fragment ds_read_b128 (16 keys at one chunk per
-// quarter-wave) and the V^T ds_read_b64_tr_b16 (4 keys x 32 bytes per
-// 16-lane group).  The row stride alone (1152 bytes) gives 4-way conflicts.
-template <int D>
-__device__ __forceinline__ int kv_swz(int k) {
-  return k & AttnShape<D>::FMASK;
-}
-template <int D>
-__device__ __forceinline__ int kv_off(int k, int c) {
-  return k * (D * 2) + ((c ^ kv_swz<D>(k)) << 4);
-}
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) const char lds_cchar;
-
-__device__ __forceinline__ uint32_t lds_addr(const char* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cchar*)p));
-}
-
-// ds_read_b64_tr_b16 issued from inline asm at LDS byte address addr + OFF.
-// Through the builtin, the compiler makes every such read wait for all
-// outstanding LDS-DMA copies (vmcnt(0)), which would serialise the gather of
-// later tiles with this tile's P.V; issued this way the read is ordered only
-// by lds_wait below.
-template <int OFF>
-__device__ __forceinline__ v4i16 tr_read(uint32_t addr) {
-  v4i16 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
-  return r;
-}
-
-// ds_read_b128 at LDS byte address addr + OFF, issued in program order (the
-// compiler would otherwise move each read next to its use and serialise the
-// S^T MFMAs behind the LDS latency).
-template <int OFF>
-__device__ __forceinline__ bf16x8 ld128(uint32_t addr) {
-  bf16x8 r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
-  return r;
-}
-
-// Waits until at most N of this wave's LDS operations are outstanding.  The
-// two registers are tied to the wait so that their uses stay after it.  LDS
-// operations complete in order, so the compiler's own lgkmcnt waits stay
-// correct (they only become stricter) with these reads in flight.
-template <int N>
-__device__ __forceinline__ void lds_wait(v4i16& x, v4i16& y) {
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
-}
-template <int N>
-__device__ __forceinline__ void lds_wait(bf16x8& x, bf16x8& y) {
-  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// A VALU instruction may read the result of a v_mfma only after the MFMA's
-// wait states (11 for an 8-pass XDL op).  The compiler does not count them
-// when the first read lands in a successor block (here: after the rescale
-// branch), so accumulators that VALU reads go through this fence: 20 wait
-// states, tied to the registers so that every read stays behind it.
-__device__ __forceinline__ void mfma_result_fence(f32x4& x, f32x4& y) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(x), "+v"(y));
-}
-
-// Two floats to packed bf16, round-to-nearest-even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
-
-// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
-template <int I, int N, typename F>
-__device__ __forceinline__ void attn_static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    attn_static_for<I + 1, N>(f);
-  }
-}
-
-// s_waitcnt immediate: vmcnt <= n (6-bit field: bits 3:0 and 15:14),
-// lgkmcnt = 0, expcnt not waited (gfx9 encoding).
-constexpr int vm_lgkm0(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4); }
-
-// Waits until at most N LDS operations of this wave are outstanding (no
-// registers tied; follow with reg_tie on the registers the wait covers).
-template <int N>
-__device__ __forceinline__ void lds_wait_n() {
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
-}
-// Keeps every use of x after the preceding inline-asm wait.
-template <typename T>
-__device__ __forceinline__ void reg_tie(T& x) {
-  asm volatile("" : "+v"(x));
-}
-
-// Tile barrier of the main loops.  __syncthreads() carries a workgroup
-// release fence, for which the compiler waits on every outstanding LDS-DMA
-// copy (vmcnt(0)) -- including the gathers just issued for later tiles, which
-// would leave no gather latency hidden.  Here each wave first waits for
-// exactly what the other waves read after the barrier (its LDS stores:
-// lgkmcnt(0); the copies of the next tile: an explicit vmcnt), and the empty
-// asm statements keep the compiler from moving memory accesses across the
-// barrier.
-__device__ __forceinline__ void attn_tile_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Threads of a workgroup: kAttnWaves S^T / softmax waves ("producers", 16
 // heads each) and kAttnWaves P.V waves ("consumers", 16-dim output blocks

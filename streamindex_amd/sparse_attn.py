@@ -1,8 +1,9 @@
-"""Sparse-attention forward on MI355X (gfx950 HIP kernel via the C ABI).
+"""Sparse attention on MI355X (gfx950 HIP kernels via the C ABI).
 
-Mirrors ``flash_sparse/triton/sparse_attn_fwd.py:180-292`` (``sparse_attn_fwd``)
-and the forward half of ``flash_sparse/triton/__init__.py:19-60``
-(``sparse_attn``).  Same argument names, shapes, dtypes and return values.
+Mirrors ``flash_sparse/triton/sparse_attn_fwd.py:180-292`` (``sparse_attn_fwd``),
+``flash_sparse/triton/sparse_attn_bwd.py:286-416`` (``sparse_attn_bwd``) and
+``flash_sparse/triton/__init__.py:19-60`` (``sparse_attn`` with autograd).
+Same argument names, shapes, dtypes and return values.
 
 Differences, all deliberate:
 
@@ -12,7 +13,11 @@ Differences, all deliberate:
   query's KV rows once for all heads, so there is no head-block knob.
 * An index ``>= N_kv`` is treated like ``-1`` (masked) instead of reading out
   of bounds.
-* ``sparse_attn`` is forward-only: calling ``backward`` raises.
+* The backward reduces dkv deterministically (per-(query, slot) rows
+  reduced key by key in a fixed order) instead of with fp32 atomics, so
+  repeated calls give bit-identical gradients; each row is rounded to bf16
+  before the fp32 sum.  Its workspace comes from the torch caching allocator
+  and long sequences are processed in chunks of query rows that fit it.
 """
 
 from __future__ import annotations
@@ -92,22 +97,105 @@ def sparse_attn_fwd(
     return o, lse
 
 
+# Default cap on the backward's workspace: at most this, and at most a quarter
+# of the device memory free at the call.
+BWD_WORKSPACE_CAP = 8 << 30
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+
+
+def sparse_attn_bwd(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    attn_sink: torch.Tensor,
+    topk_idxs: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    do: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    *,
+    block_h: Optional[int] = None,
+    workspace_bytes: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of :func:`sparse_attn_fwd` from its saved ``o`` and ``lse``.
+
+    Returns ``(dq, dkv, dattn_sink)`` shaped and typed like ``q``, ``kv`` and
+    ``attn_sink``.  ``workspace_bytes`` caps the scratch memory (default:
+    ``BWD_WORKSPACE_CAP`` or a quarter of the free device memory, whichever is
+    smaller); the query rows are processed in as few chunks as fit it.
+    """
+    del block_h
+    assert q.is_cuda and kv.is_cuda and do.is_cuda
+    assert q.shape == do.shape, "do must match q shape"
+    assert q.dtype == kv.dtype == do.dtype
+    assert attn_sink.dtype == torch.float32
+    assert lse.dtype == torch.float32
+    assert q.dim() == 4 and kv.dim() == 3 and topk_idxs.dim() == 3
+    B, S, H, D = q.shape
+    B2, N_kv, D2 = kv.shape
+    assert B2 == B and D2 == D, "q and kv shape mismatch"
+    assert o.shape == q.shape and o.dtype == q.dtype
+    assert lse.shape == (B, S, H) and attn_sink.shape == (H,)
+    assert topk_idxs.shape[:2] == (B, S)
+    if q.dtype != torch.bfloat16:
+        raise ValueError("only bfloat16 q/kv are supported on MI355X")
+    if D not in SUPPORTED_D:
+        raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
+    if H > MAX_HEADS:
+        raise ValueError(f"H ({H}) must be <= {MAX_HEADS}")
+    if topk_idxs.dtype not in (torch.int32, torch.int64):
+        topk_idxs = topk_idxs.to(torch.int64)
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    K = topk_idxs.shape[-1]
+    q, kv, o, do = (t if _aligned(t) else t.contiguous() for t in (q, kv, o, do))
+    attn_sink = attn_sink.contiguous()
+    dq = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
+    dkv = torch.empty((B, N_kv, D), dtype=kv.dtype, device=q.device)
+    dsink = torch.empty((H,), dtype=torch.float32, device=q.device)
+    L = _lib.load()
+    with torch.cuda.device(q.device):
+        if workspace_bytes is None:
+            free, _ = torch.cuda.mem_get_info(q.device)
+            workspace_bytes = min(BWD_WORKSPACE_CAP, free // 4)
+        need = L.si_sparse_attn_bwd_workspace_bytes(B, S, H, D, N_kv, K, int(workspace_bytes))
+        if need < 0:
+            raise ValueError(L.si_last_error().decode("utf-8", "replace"))
+        ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=q.device)
+        rc = L.si_sparse_attn_bwd(
+            q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
+            topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
+            o.data_ptr(), _lib.strides(o), lse.data_ptr(), _lib.strides(lse), do.data_ptr(), _lib.strides(do),
+            B, S, H, D, N_kv, K, float(softmax_scale), dq.data_ptr(), _lib.strides(dq),
+            dkv.data_ptr(), _lib.strides(dkv), dsink.data_ptr(), ws.data_ptr(), ws.numel(),
+            _lib.stream_ptr(q.device))
+    _lib.check(rc)
+    return dq, dkv, dsink
+
+
 class _SparseAttnFunc(torch.autograd.Function):
-    """Forward-only autograd wrapper (``flash_sparse/triton/__init__.py:19-44``)."""
+    """``flash_sparse/triton/__init__.py:19-44``: saves q, kv, attn_sink,
+    topk_idxs, o and lse for the backward."""
 
     @staticmethod
     def forward(ctx, q, kv, attn_sink, topk_idxs, softmax_scale):
-        o, _ = sparse_attn_fwd(q, kv, attn_sink, topk_idxs, softmax_scale)
+        o, lse = sparse_attn_fwd(q, kv, attn_sink, topk_idxs, softmax_scale)
+        ctx.save_for_backward(q, kv, attn_sink, topk_idxs, o, lse)
+        ctx.softmax_scale = softmax_scale
         return o
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError("sparse_attn backward is not implemented on MI355X (forward-only hot path)")
+        q, kv, attn_sink, topk_idxs, o, lse = ctx.saved_tensors
+        dq, dkv, dsink = sparse_attn_bwd(q, kv, attn_sink, topk_idxs, o, lse, do.contiguous(), ctx.softmax_scale)
+        return dq, dkv, dsink, None, None
 
 
 def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = None) -> torch.Tensor:
-    """Sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``)."""
+    """Differentiable sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``)."""
     return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale)
 
 
-__all__ = ["sparse_attn_fwd", "sparse_attn"]
+__all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn"]

@@ -144,7 +144,7 @@ def test_v4_shape_with_indexer_indices(cuda_device):
     _check(q, kv, sink, idx, 576 ** -0.5, o, lse, "v4")
 
 
-def test_sparse_attn_forward_only(cuda_device):
+def test_sparse_attn_matches_fwd(cuda_device):
     B, S, H, D, N, K = 1, 4, 16, 64, 32, 8
     q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=7)
     idx = synth.causal_random_topk(B, S, K, 1, seed=7)
