@@ -65,7 +65,7 @@ struct AttnBwdArgs {
   int64_t dqsb, dqss, dqsh;
   float* dsink_rows;   // [B*S, 64*HG]: -e^{sink-lse} delta per (row, head)
   uint16_t* coef;      // [nrows, HG, ntiles, 2, 4, 64, 8] bf16: P, dS fragments
-  uint16_t* prow;      // [nrows, HG, K, D] bf16: per-(query, slot) dkv rows
+  uint16_t* prow;      // [nrows, HG, 32 ntiles, D] bf16: per-(query, slot) dkv rows
   int B, S, H, N, K, HG, ntiles;
   int64_t row0;        // first global row (b*S + s) of this chunk
   int nrows;           // rows in this chunk
@@ -484,19 +484,32 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
   const int ntiles = a.ntiles;
   constexpr int CPR = D / 8;
 
-  // Q and dO of the row's 64 heads into LDS (zero past H)
-  for (int e = threadIdx.x; e < 2 * 64 * CPR; e += kRowsThreads) {
-    const int m = e / (64 * CPR);
-    const int h = (e / CPR) % 64;
-    const int c = e % CPR;
-    const int hq = hbase + h;
-    u32x4 v{0u, 0u, 0u, 0u};
-    if (hq < a.H) {
+  // Q and dO of the row's 64 heads into LDS (zero past H).  Every load of a
+  // thread is issued before its first LDS store (one wave per SIMD leaves the
+  // registers), so the row's 2 x 64 x D elements arrive in one round trip.
+  {
+    constexpr int PER = 2 * 64 * CPR / kRowsThreads;  // 16-byte chunks per thread (CPR is even)
+    static_assert(2 * 64 * CPR % kRowsThreads == 0, "chunks must divide over the threads");
+    u32x4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = i * kRowsThreads + static_cast<int>(threadIdx.x);
+      const int m = e / (64 * CPR);
+      const int h = (e / CPR) % 64;
+      const int c = e % CPR;
+      const int hq = hbase + h;
       const uint16_t* src = m == 0 ? a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh
                                    : a.dout + b * a.gsb + static_cast<int64_t>(s) * a.gss + static_cast<int64_t>(hq) * a.gsh;
-      v = *reinterpret_cast<const u32x4*>(src + c * 8);
+      v[i] = hq < a.H ? *reinterpret_cast<const u32x4*>(src + c * 8) : u32x4{0u, 0u, 0u, 0u};
     }
-    *reinterpret_cast<u32x4*>(qd_lds + m * DS::QD + h * DS::QROW + c * 16) = v;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = i * kRowsThreads + static_cast<int>(threadIdx.x);
+      const int m = e / (64 * CPR);
+      const int h = (e / CPR) % 64;
+      const int c = e % CPR;
+      *reinterpret_cast<u32x4*>(qd_lds + m * DS::QD + h * DS::QROW + c * 16) = v[i];
+    }
   }
   const uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * ntiles * kCoefTile;
   // each thread moves 2 x 16 bytes of a tile's coefficient block
@@ -529,24 +542,10 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
   const int bh = 8 * g + (i16 >> 2);
   const uint32_t cf0 = lds_addr(coef_lds) + ((bh >> 4) * 64 + (i16 & 3) * 16 + (bh & 15)) * 16;
 
-  const int64_t prow_base = (static_cast<int64_t>(lrow) * a.HG + hg) * a.K;
-  const int64_t irow = b * a.isb + static_cast<int64_t>(s) * a.iss;
+  const int64_t prow_base = (static_cast<int64_t>(lrow) * a.HG + hg) * (static_cast<int64_t>(ntiles) * kAttnTK);
 
   for (int t = 0; t < ntiles; ++t) {
     if (t + 1 < ntiles) coef_load(t + 1);
-    // validity of this lane's two output keys
-    bool kval[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int j = t * kAttnTK + nb * 16 + i16;
-      bool ok = false;
-      if (j < a.K) {
-        const int64_t raw = a.idx64 ? static_cast<const int64_t*>(a.idx)[irow + j * a.isk]
-                                    : static_cast<int64_t>(static_cast<const int32_t*>(a.idx)[irow + j * a.isk]);
-        ok = raw >= 0 && raw < a.N;
-      }
-      kval[nb] = ok;
-    }
     // k-steps 0, 1: dS of heads 0..31, 32..63 against Q; 2, 3: P against dO
     bf16x8 bfr[4][2];
     auto b_read = [&](auto KC, auto NC) {
@@ -598,22 +597,25 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
           acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[kst][0], acc[0], 0, 0, 0);
           acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[kst][1], acc[1], 0, 0, 0);
         }
-        // lane (key 16nb + i16, g) holds dimensions 16 mbi + 4g + 0..3
+        // lane (key 16nb + i16, g) holds dimensions 16 mbi + 4g + 0..3.  Every
+        // slot of the padded tile is written: a masked or padding slot has
+        // P = dS = 0 and no key, so the reduction never reads its row, and
+        // unconditional stores keep the prefetch waits exact.
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          if (kval[nb]) {
-            uint2 w;
-            w.x = f32x2_to_bf16x2(acc[nb][0], acc[nb][1]);
-            w.y = f32x2_to_bf16x2(acc[nb][2], acc[nb][3]);
-            *reinterpret_cast<uint2*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + mbi * 16 + 4 * g) = w;
-          }
+          uint2 w;
+          w.x = f32x2_to_bf16x2(acc[nb][0], acc[nb][1]);
+          w.y = f32x2_to_bf16x2(acc[nb][2], acc[nb][3]);
+          *reinterpret_cast<uint2*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + mbi * 16 + 4 * g) = w;
         }
       }
     };
     attn_static_for<0, MBW>(block);
-    __syncthreads();  // every wave is done with this tile's coefficients
+    // Barriers without a release fence: they order only LDS (the row stores
+    // need no ordering), so the stores of this tile stay in flight.
+    attn_tile_barrier();  // every wave is done with this tile's coefficients
     if (t + 1 < ntiles) coef_store();
-    __syncthreads();
+    attn_tile_barrier();
   }
 }
 
@@ -624,11 +626,11 @@ struct DkvReduceArgs {
   const uint32_t* pair;   // local pair ids (lrow K + j) sorted by key
   const int32_t* seg_lo;  // per key id b N + t: its pairs are pair[seg_lo, seg_hi)
   const int32_t* seg_hi;
-  const uint16_t* prow;   // [nrows, HG, K, D]
+  const uint16_t* prow;   // [nrows, HG, KP, D]
   float* acc;             // [B N, D] running fp32 sum across chunks
   uint16_t* dkv;          // [B, N, D] bf16
   int64_t dsb, dsn;
-  int K, HG, N;
+  int K, KP, HG, N;      // KP: slots per (row, head group), K rounded up to whole tiles
   int first, last;        // first / last chunk of query rows
 };
 
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(kReduceThreads) void sparse_attn_bwd_dkv_reduce_ker
       const int64_t lrow = pid / static_cast<uint32_t>(r.K);
       const int64_t j = pid % static_cast<uint32_t>(r.K);
       for (int h = 0; h < r.HG; ++h) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(r.prow + ((lrow * r.HG + h) * r.K + j) * D + c * 8);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(r.prow + ((lrow * r.HG + h) * r.KP + j) * D + c * 8);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           sum[2 * e] += bf_lo(v[e]);
@@ -790,7 +792,7 @@ static int bwd_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64
   p->seg_hi = take(static_cast<size_t>(nkeys) * 4);
   const size_t npairs = ntiles > 0 ? static_cast<size_t>(rows) * K : 0;
   p->coef = take(static_cast<size_t>(rows) * HG * ntiles * kCoefTile * 2);
-  p->prow = take(ntiles > 0 ? static_cast<size_t>(rows) * HG * K * D * 2 : 0);
+  p->prow = take(static_cast<size_t>(rows) * HG * ntiles * kAttnTK * D * 2);
   p->kin = take(npairs * 4);
   p->kout = take(npairs * 4);
   p->vin = take(npairs * 4);
@@ -894,6 +896,7 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     r.dsb = dkvsb;
     r.dsn = dkvsn;
     r.K = a.K;
+    r.KP = a.ntiles * kAttnTK;
     r.HG = a.HG;
     r.N = a.N;
     r.first = row0 == 0;
