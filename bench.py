@@ -16,7 +16,9 @@ Printed (one JSON line, rank 0):
   parity         recall vs the CPU oracle on sampled rows
   cpu_baseline   the CPU oracle on a bounded row sample, extrapolated
   extra          S=1M indexer time (config[4] indexer stage), sparse-attn fwd
-                 at config[3] with its HBM roofline, and the end-to-end CSA
+                 at config[3] with its HBM roofline, the sparse-attn backward
+                 at config[3] (dq, dkv, dsink from the saved o / lse; sampled
+                 dq rows and dkv keys against the oracle), and the end-to-end CSA
                  forward (flash_csa_forward: fused indexer -> int32 window +
                  compressed index rows -> sparse attention, 64 heads, d=576,
                  n_win=128) at S=64K and at S=1M (config[4]) with its stage
@@ -37,7 +39,8 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from streamindex_amd import chunked_indexer_topk, csa_topk_idxs, flash_csa_forward, sparse_attn, sparse_attn_fwd  # noqa: E402,E501
+from streamindex_amd import (chunked_indexer_topk, csa_topk_idxs, flash_csa_forward, sparse_attn,  # noqa: E402
+                             sparse_attn_bwd, sparse_attn_fwd)
 from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
 
@@ -129,20 +132,70 @@ def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, s
     return dict(q=q, k=k, w=w, T=T, ms=ms, wall_ms=wall, peak_gib=peak, flops=flops, idx=idx, sc=sc)
 
 
-def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None):
+def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True):
+    """Forward (and optionally backward) sparse attention at one shape.  The
+    backward is timed from the forward's saved (o, lse) with dO ~ N(0,1)·0.5,
+    including its key sort and reduction; its FLOPs count the five products
+    per selected (row, key) pair (S and dP recomputed, dQ, dK, dV): 10 H D."""
     dev = torch.device("cuda:0")
     q, kv, sink = synth.sparse_attn_inputs(1, S, H, D, T, seed=2027, device=dev)
     if idx is None:
         idx = synth.causal_random_topk(1, S, top_k, 4, device=dev)
     fn = lambda: sparse_attn_fwd(q, kv, sink, idx, D ** -0.5)  # noqa: E731
-    for _ in range(max(1, warmup)):
-        fn()
-    torch.cuda.synchronize()
-    ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
     nvalid = float((idx >= 0).sum().item())
-    flops = 4.0 * H * D * nvalid
-    unique_bytes = (q.numel() * 2 * 2 + idx.numel() * idx.element_size() + S * H * 4 + kv.numel() * 2)
-    return dict(ms=ms, flops=flops, unique_bytes=unique_bytes, nvalid=nvalid)
+    res = dict(nvalid=nvalid)
+    stream = torch.cuda.current_stream(dev)
+    if fwd:
+        for _ in range(max(1, warmup)):
+            fn()
+        torch.cuda.synchronize()
+        res["ms"] = _events_time(fn, steps, stream)
+        res["flops"] = 4.0 * H * D * nvalid
+        res["unique_bytes"] = (q.numel() * 2 * 2 + idx.numel() * idx.element_size() + S * H * 4 + kv.numel() * 2)
+    if bwd:
+        o, lse = fn()
+        g = torch.Generator(device=dev)
+        g.manual_seed(2028)
+        do = torch.randn(q.shape, generator=g, device=dev, dtype=torch.bfloat16).mul_(0.5)
+        bfn = lambda: sparse_attn_bwd(q, kv, sink, idx, o, lse, do, D ** -0.5)  # noqa: E731
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        for _ in range(max(1, warmup)):
+            grads = bfn()
+        del grads
+        torch.cuda.synchronize()
+        res["bwd_ms"] = _events_time(bfn, steps, stream)
+        res["bwd_flops"] = 10.0 * H * D * nvalid
+        res["bwd_peak_extra_gib"] = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+        res["bwd_parity"] = attn_bwd_check(q, kv, sink, idx, o, lse, do, bfn())
+    return res
+
+
+def attn_bwd_check(q, kv, sink, idx, o, lse, do, grads, nrows=2, nkeys=2, seed=6):
+    """dq on sampled rows and dkv on sampled late keys (few rows select them)
+    against the oracle backward; relative Frobenius and max errors."""
+    from oracle import oracle as O
+
+    dq, dkv, _ = grads
+    S, N, D = q.shape[1], kv.shape[1], q.shape[3]
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(S, size=nrows, replace=False))
+    keys = np.sort(N - 1 - rng.choice(N // 16, size=nkeys, replace=False))
+    sel = torch.from_numpy(rows).to(q.device)
+    idx_c = idx[0].cpu().numpy().astype(np.int64)
+    hit = np.nonzero(np.isin(idx_c, keys).any(axis=1))[0]
+    ht = torch.from_numpy(hit).to(q.device)
+    sk = sink.cpu().numpy()
+    rdq, _, _ = O.sparse_attn_bwd_rows(_bits(q[0, sel]), _bits(kv[0]), _bits(o[0, sel]), _bits(do[0, sel]), sk,
+                                       lse[0, sel].cpu().numpy(), idx_c[rows], D ** -0.5, want_dkv=False)
+    _, rdkv, _ = O.sparse_attn_bwd_rows(_bits(q[0, ht]), _bits(kv[0]), _bits(o[0, ht]), _bits(do[0, ht]), sk,
+                                        lse[0, ht].cpu().numpy(), idx_c[hit], D ** -0.5, keys=keys, want_dq=False)
+    out = {"dq_rows": int(nrows), "dkv_keys": int(nkeys), "dkv_key_rows": int(len(hit))}
+    for name, got, ref in (("dq", dq[0, sel].float().cpu().numpy(), rdq),
+                           ("dkv", dkv[0, torch.from_numpy(keys).to(q.device)].float().cpu().numpy(), rdkv)):
+        out[f"{name}_rel_fro"] = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+        out[f"{name}_max_rel"] = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+    return out
 
 
 def csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m, nrows, seed=3):
@@ -239,6 +292,8 @@ def main():
     ap.add_argument("--no-attn", action="store_true", help="skip the sparse-attention measurement")
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
     ap.add_argument("--only-attn", action="store_true", help="sparse-attention timing only (for profilers)")
+    ap.add_argument("--only-attn-bwd", action="store_true", help="sparse-attention backward timing only (for profilers)")
+    ap.add_argument("--no-attn-bwd", action="store_true", help="skip the sparse-attention backward measurement")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end CSA forward measurements")
     ap.add_argument("--e2e-parity-rows", type=int, default=1024,
                     help="sampled rows for the S=1M end-to-end recall check (config[4] asks 1024)")
@@ -259,6 +314,11 @@ def main():
     if args.only_e2e:
         re_ = run_csa_e2e(args.only_e2e, args.steps, args.warmup, 0)
         print(json.dumps({k: v for k, v in re_.items() if not isinstance(v, dict)}), flush=True)
+        return
+    if args.only_attn_bwd:
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, bwd=True, fwd=False)
+        print(json.dumps({"sparse_attn_bwd_ms": ra["bwd_ms"], "tflops": ra["bwd_flops"] / ra["bwd_ms"] / 1e9,
+                          "parity": ra["bwd_parity"]}), flush=True)
         return
     if args.only_attn:
         ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup)
@@ -305,8 +365,14 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_attn:
         print("[bench] sparse attention config[3]", file=sys.stderr, flush=True)
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1)
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1, bwd=not args.no_attn_bwd)
         extra["sparse_attn_ms"] = ra["ms"]
+        if "bwd_ms" in ra:
+            extra["sparse_attn_bwd_ms"] = ra["bwd_ms"]
+            extra["sparse_attn_bwd_tflops"] = ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12
+            extra["sparse_attn_bwd_mfma_frac"] = extra["sparse_attn_bwd_tflops"] / PEAK_BF16_TFLOPS
+            extra["sparse_attn_bwd_peak_extra_gib"] = ra["bwd_peak_extra_gib"]
+            extra["sparse_attn_bwd_parity"] = ra["bwd_parity"]
         extra["sparse_attn_tflops"] = ra["flops"] / (ra["ms"] * 1e-3) / 1e12
         extra["sparse_attn_unique_gbps"] = ra["unique_bytes"] / (ra["ms"] * 1e-3) / 1e9
         extra["sparse_attn_hbm_frac"] = extra["sparse_attn_unique_gbps"] / PEAK_HBM_GBPS
