@@ -13,8 +13,10 @@
 // S^T/softmax "producer" waves and four P.V "consumer" waves, one of each per
 // SIMD, so the matrix cores of a SIMD alternate between the two roles):
 //   * The row's top-k KV rows are gathered 32 at a time straight from L2/HBM
-//     into a 4-slot LDS ring with global_load_lds (no staging registers),
-//     three tiles ahead of use; each row is read once per query for all heads.
+//     into a 4-slot LDS ring with global_load_lds (no staging registers) by
+//     the producers, three tiles ahead of use; each row is read once per query
+//     for all heads.  The tile barrier carries no release fence, so the copies
+//     of later tiles stay in flight across it.
 //     Rows are stored key-major with a per-key XOR swizzle of the 16-byte
 //     chunks so that both LDS read patterns below are bank-conflict-free.
 //   * S^T = K·Q^T (v_mfma_f32_16x16x32_bf16, keys on M, heads on N), split
@@ -29,8 +31,8 @@
 //     tile.
 //   * O^T = V^T·P^T, split across the consumers by output dimension (the
 //     16-dim blocks are dealt round-robin), so every V element is read from
-//     LDS once.  The consumers also issue the KV gathers and run the index
-//     pipeline, so each role needs at most ~210 VGPRs and two waves fit a SIMD.
+//     LDS once.  The first consumer wave runs the index pipeline; each role
+//     needs at most ~210 VGPRs and two waves fit a SIMD.
 //     The V^T A-fragments are read from the key-major tile with
 //     ds_read_b64_tr_b16 (two transposing reads give a lane 8 keys of one
 //     dimension); the P^T B-fragments use the key order of the score
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   // Tile protocol (one barrier per tile).  Iteration `it`: the consumers
   // compute P.V of tile it while the producers compute S^T + softmax of tile
   // it+1 and publish its P^T and rescale factors; tile t lives in ring slot
-  // t % 4 and its P^T in p_lds[t % 2].  The consumers issue the copies of
+  // t % 4 and its P^T in p_lds[t % 2].  The producers issue the copies of
   // tile it+3 at the start of the iteration into the slot of tile it-1
   // (finished by every wave in iteration it-1); they must land by the end of
   // iteration it+1, two iterations of gather latency.  The first consumer
