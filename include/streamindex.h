@@ -167,6 +167,46 @@ int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, 
                        const int64_t* dkv_strides, float* dsink, void* workspace, int64_t workspace_bytes,
                        void* stream);
 
+/*
+ * Block quantise-dequantise simulations, bit-identical to the reference formulas.
+ * Replaces flash_sparse/utils/quantization.py:19-37 (fp4 = 0: act_quant_simulate,
+ * fp8 e4m3, scale = amax / 448) and :40-65 (fp4 = 1: fp4_act_quant_simulate,
+ * e2m1 grid, scale = amax / 6).
+ *   x, y: n contiguous elements of dtype 0 = fp32, 1 = bf16, 2 = fp16; blocks of
+ *   block_size consecutive elements (block_size = 8 * 2^j <= 512, n % block_size == 0).
+ */
+int si_quant_simulate(const void* x, void* y, int dtype, int64_t n, int64_t block_size, int fp4, void* stream);
+
+/*
+ * Packed production formats named by flash_sparse/utils/quantization.py:3-9
+ * (DeepSeek-V4 act_quant / fp4_act_quant).
+ *   fp4 = 0: y = n fp8 e4m3 bytes, scale[n / block_size] fp32 = max(amax, 1e-4) / 448
+ *            (pow2_scale: rounded up to a power of two, UE8M0);
+ *   fp4 = 1: y = n / 2 bytes of e2m1 pairs (element 2i in the low nibble),
+ *            scale = power of two >= max(amax, 6 * 2^-126) / 6.
+ *   Values are rounded to nearest, ties to even.
+ */
+int si_quant_pack(const void* x, void* y, float* scale, int dtype, int64_t n, int64_t block_size, int fp4,
+                  int pow2_scale, void* stream);
+
+/*
+ * Token compressor (softmax-gated pooling of m tokens into one entry).
+ * Replaces flash_sparse/reference.py:176-272 (reference_token_compressor).
+ *   c_a, z_a [B,S,C] (dtype as above), b_a [m,C] fp32; overlap = 1 (CSA, eq. 11-12)
+ *   also c_b, z_b [B,S,C] and b_b [m,C]: entry i pools block i of stream a and
+ *   block i-1 of stream b (none for i = 0).  out [B, S/m, C] (trailing tokens dropped).
+ */
+int si_token_compress(const void* c_a, const void* z_a, const float* b_a, const void* c_b, const void* z_b,
+                      const float* b_b, int dtype, int64_t B, int64_t S, int64_t C, int64_t m, int overlap, void* out,
+                      void* stream);
+
+/*
+ * out[o, i] = sum_l kv[o, l, i] softmax_l(score[o, :, i]) over contiguous [outer, L, inner].
+ * Replaces flash_sparse/utils/compression.py:13-24 (softmax_gated_pool).
+ */
+int si_gated_pool(const void* kv, const void* score, void* out, int dtype, int64_t outer, int64_t L, int64_t inner,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,10 @@ Reference semantics followed (file:line in the reference tree):
   LSE: ``flash_sparse/triton/sparse_attn_fwd.py:148-177``;
 * sparse-attention backward from the saved (o, lse):
   ``flash_sparse/triton/sparse_attn_bwd.py:1-26,93-97,224-283``;
+* fp8 / fp4 quantisation: ``flash_sparse/utils/quantization.py:19-65`` (the
+  simulations, with the rounding of every torch op to the input dtype) and the
+  packed production formats its docstring names (``quantization.py:3-9``);
+  the token compressor: ``flash_sparse/reference.py:176-272``;
 * CSA / HCA attention index rows: ``flash_sparse/csa.py:30-83,176-179``,
   ``flash_sparse/hca.py:24-51``, window ``flash_sparse/reference.py:460-475``.
 
@@ -316,6 +320,128 @@ def np_sparse_attn_bwd(qf, kvf, of, dof, sink, lse, idx, scale: float):
     np.add.at(dkv, safe[valid], contrib[valid])
     dsink = -(np.exp(sink[None, :] - lse) * delta).sum(0)
     return dq, dkv, dsink
+
+
+# ---------------------------------------------------------------------------
+# FP8 / FP4 quantisation (utils/quantization.py) and the token compressor
+# ---------------------------------------------------------------------------
+FP4_GRID = np.array([-6, -4, -3, -2, -1.5, -1, -0.5, 0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=np.float64)
+FP4_CODES = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, 0, -0.5, -1, -1.5, -2, -3, -4, -6], dtype=np.float64)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to bf16 / fp16 (nearest, ties to even) or keep fp32;
+    returns float32."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "float32":
+        return x
+    if dtype == "float16":
+        return x.astype(np.float16).astype(np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def e4m3_round(x: np.ndarray) -> np.ndarray:
+    """Nearest OCP fp8 e4m3 value (bias 7, 3 mantissa bits, subnormal step
+    2^-9, max 448), ties to even; |x| <= 448 expected."""
+    x = np.asarray(x, dtype=np.float64)
+    a = np.abs(x)
+    with np.errstate(divide="ignore"):
+        ex = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    ex = np.maximum(ex, -6)
+    q = np.exp2(ex - 3)
+    r = np.minimum(np.round(a / q) * q, 448.0)  # np.round: ties to even
+    return np.where(a > 0, np.copysign(r, x), x)
+
+
+def act_quant_simulate(x: np.ndarray, dtype: str, block_size: int = 128) -> np.ndarray:
+    """quantization.py:19-37 with every torch op rounded to ``dtype``."""
+    x = np.asarray(x, dtype=np.float32)
+    blk = x.reshape(*x.shape[:-1], -1, block_size)
+    amax = round_to(np.maximum(np.abs(blk).max(-1, keepdims=True), np.float32(1e-4)), dtype)
+    scale = round_to(amax / np.float32(448.0), dtype)
+    y = np.clip(round_to(blk / scale, dtype), -448.0, 448.0)
+    q = e4m3_round(y).astype(np.float32)
+    return round_to(q * scale, dtype).reshape(x.shape)
+
+
+def fp4_act_quant_simulate(x: np.ndarray, dtype: str, block_size: int = 32) -> np.ndarray:
+    """quantization.py:40-65 with every torch op rounded to ``dtype`` (argmin
+    over the diffs rounded to ``dtype``; first minimum wins)."""
+    x = np.asarray(x, dtype=np.float32)
+    blk = x.reshape(*x.shape[:-1], -1, block_size)
+    amax = round_to(np.maximum(np.abs(blk).max(-1, keepdims=True), np.float32(6 * 2.0 ** -126)), dtype)
+    scale = round_to(amax / np.float32(6.0), dtype)
+    y = np.clip(round_to(blk / scale, dtype), -6.0, 6.0)
+    diffs = np.abs(round_to(y[..., None] - FP4_GRID.astype(np.float32), dtype))
+    q = FP4_GRID.astype(np.float32)[np.argmin(diffs, axis=-1)]
+    return round_to(q * scale, dtype).reshape(x.shape)
+
+
+def fp8_pack(x: np.ndarray, block_size: int = 128, pow2: bool = False):
+    """Production fp8: (e4m3 values as float64, fp32 scale per block)."""
+    x = np.asarray(x, dtype=np.float32)
+    blk = x.reshape(*x.shape[:-1], -1, block_size)
+    amax = np.maximum(np.abs(blk).max(-1, keepdims=True), np.float32(1e-4))
+    scale = (amax / np.float32(448.0)).astype(np.float32)
+    if pow2:
+        scale = np.exp2(np.ceil(np.log2(scale.astype(np.float64)))).astype(np.float32)
+    y = np.clip((blk / scale).astype(np.float32), -448.0, 448.0)
+    return e4m3_round(y).reshape(x.shape), scale[..., 0]
+
+
+def e2m1_round(y: np.ndarray) -> np.ndarray:
+    """Nearest e2m1 value, ties to the even code (0, 1, 2, 4 have even codes)."""
+    a = np.abs(np.asarray(y, dtype=np.float64))
+    mags = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6])
+    d = np.abs(a[..., None] - mags)
+    best = d.min(-1, keepdims=True)
+    tie_ok = (d == best) & ((np.arange(8) % 2) == 0)      # prefer an even code among ties
+    idx = np.where(tie_ok.any(-1), np.argmax(tie_ok, -1), np.argmin(d, -1))
+    return np.copysign(mags[idx], y) * (mags[idx] > 0)
+
+
+def fp4_pack(x: np.ndarray, block_size: int = 32):
+    """Production fp4: (e2m1 values as float64, power-of-two fp32 scale per block)."""
+    x = np.asarray(x, dtype=np.float32)
+    blk = x.reshape(*x.shape[:-1], -1, block_size)
+    amax = np.maximum(np.abs(blk).max(-1, keepdims=True), np.float32(6 * 2.0 ** -126))
+    ratio = (amax / np.float32(6.0)).astype(np.float32).astype(np.float64)
+    scale = np.exp2(np.ceil(np.log2(ratio))).astype(np.float32)
+    return e2m1_round((blk / scale).astype(np.float32)).reshape(x.shape), scale[..., 0]
+
+
+def fp4_unpack(packed: np.ndarray) -> np.ndarray:
+    """uint8 [..., n/2] (element 2i in the low nibble) -> e2m1 values [..., n]."""
+    p = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,))
+    out[..., 0::2] = FP4_CODES[p & 15]
+    out[..., 1::2] = FP4_CODES[p >> 4]
+    return out
+
+
+def token_compressor(c_a, z_a, b_a, m, c_b=None, z_b=None, b_b=None, overlap=False):
+    """reference.py:176-272 in float64 (overlap: block i pools [block i of a ;
+    block i-1 of b], block 0's b half empty)."""
+    c_a, z_a, b_a = (np.asarray(t, dtype=np.float64) for t in (c_a, z_a, b_a))
+    B, S, C = c_a.shape
+    n = S // m
+    ca = c_a[:, :n * m].reshape(B, n, m, C)
+    za = z_a[:, :n * m].reshape(B, n, m, C) + b_a
+    if not overlap:
+        w = np.exp(za - za.max(2, keepdims=True))
+        return (ca * w).sum(2) / w.sum(2)
+    cb = np.asarray(c_b, dtype=np.float64)[:, :n * m].reshape(B, n, m, C)
+    zb = np.asarray(z_b, dtype=np.float64)[:, :n * m].reshape(B, n, m, C) + np.asarray(b_b, dtype=np.float64)
+    cbs = np.zeros_like(cb)
+    cbs[:, 1:] = cb[:, :-1]
+    zbs = np.full_like(zb, -np.inf)
+    zbs[:, 1:] = zb[:, :-1]
+    cj = np.concatenate([ca, cbs], 2)
+    zj = np.concatenate([za, zbs], 2)
+    w = np.exp(zj - zj.max(2, keepdims=True))
+    return (cj * w).sum(2) / w.sum(2)
 
 
 # ---------------------------------------------------------------------------
