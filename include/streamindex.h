@@ -168,6 +168,24 @@ int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, 
                        void* stream);
 
 /*
+ * Indexer + exact top-k over quantised inputs (the production V4 indexer
+ * dtypes: fp4 queries, fp8 keys).  Same operator as si_indexer_topk
+ * (flash_sparse/triton/chunked_indexer.py:47-160) on the dequantised values
+ * q = e2m1 * q_scale, k = e4m3 * k_scale.
+ *   q_fp4 [B,S,H,D/2] uint8 (element 2i in the low nibble), byte strides q_strides[4];
+ *   q_scale [B,S,H,D/32] fp32 powers of two (their exponent bits are used as UE8M0);
+ *   k_fp8 [B,T,D] e4m3 bytes, byte strides k_strides[3]; k_scale [B,T] fp32 > 0;
+ *   weights, causal_mask, causal_ratio, outputs: as si_indexer_topk.
+ * Supported: H <= 64, D = 128, 1 <= top_k <= 2048; byte strides multiples of 16.
+ */
+int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* q_scale,
+                      const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides,
+                      const float* k_scale, const int64_t* k_scale_strides, const void* weights, int w_dtype,
+                      const int64_t* w_strides, const uint8_t* causal_mask, const int64_t* mask_strides, int64_t B,
+                      int64_t S, int64_t T, int64_t H, int64_t D, int64_t top_k, int64_t causal_ratio,
+                      int64_t* out_idx, float* out_scores, void* stream);
+
+/*
  * Block quantise-dequantise simulations, bit-identical to the reference formulas.
  * Replaces flash_sparse/utils/quantization.py:19-37 (fp4 = 0: act_quant_simulate,
  * fp8 e4m3, scale = amax / 448) and :40-65 (fp4 = 1: fp4_act_quant_simulate,

@@ -176,3 +176,112 @@ def indexer_score_topk(
 
 
 __all__ = ["chunked_indexer_topk", "indexer_score", "indexer_score_topk"]
+
+
+# ---------------------------------------------------------------------------
+# Quantised inputs (the production V4 indexer dtypes)
+# ---------------------------------------------------------------------------
+def indexer_topk_q(
+    q_fp4: torch.Tensor,
+    q_scale: torch.Tensor,
+    k_fp8: torch.Tensor,
+    k_scale: torch.Tensor,
+    weights: torch.Tensor,
+    top_k: int,
+    *,
+    causal_mask: Optional[torch.Tensor] = None,
+    causal_ratio: Optional[int] = None,
+    check_scales: bool = True,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Indexer + exact top-k over fp4 queries and fp8 keys.
+
+    Args:
+      q_fp4: ``[B, S, H_I, 64]`` uint8, e2m1 pairs (element 2i in the low
+        nibble) of ``D_I = 128`` dims, as :func:`streamindex_amd.quant.fp4_act_quant`
+        writes them.  q_scale: ``[B, S, H_I, 4]`` fp32, one power-of-two scale
+        per 32 dims.
+      k_fp8: ``[B, T, 128]`` ``torch.float8_e4m3fn``.  k_scale: ``[B, T]`` or
+        ``[B, T, 1]`` fp32, one positive scale per key row
+        (:func:`streamindex_amd.quant.act_quant` with ``block_size=128``).
+      weights, top_k, causal_mask, causal_ratio: as :func:`chunked_indexer_topk`.
+      check_scales: verify that ``q_scale`` holds powers of two (the kernel
+        reads their exponent bits as UE8M0 scales).
+
+    Returns ``(idx, scores)`` exactly as :func:`chunked_indexer_topk` does for
+    the dequantised inputs ``q = value · q_scale``, ``k = value · k_scale``.
+    """
+    assert q_fp4.is_cuda and k_fp8.is_cuda and weights.is_cuda
+    assert q_fp4.dim() == 4 and k_fp8.dim() == 3 and weights.dim() == 3
+    B, S, H_I, Dh = q_fp4.shape
+    B2, T, D_I = k_fp8.shape
+    assert B2 == B and D_I == 2 * Dh, f"q/k shape mismatch: q={tuple(q_fp4.shape)}, k={tuple(k_fp8.shape)}"
+    assert weights.shape == (B, S, H_I)
+    assert q_scale.shape == (B, S, H_I, D_I // 32), f"q_scale must be [B,S,H_I,{D_I // 32}]"
+    if k_scale.dim() == 3:
+        assert k_scale.shape[2] == 1, "one key scale per row (act_quant block_size = D_I)"
+        k_scale = k_scale[..., 0]
+    assert k_scale.shape == (B, T)
+    if q_fp4.dtype != torch.uint8 or k_fp8.dtype != torch.float8_e4m3fn:
+        raise ValueError(f"q_fp4 must be uint8 and k_fp8 float8_e4m3fn, got {q_fp4.dtype} / {k_fp8.dtype}")
+    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
+        raise ValueError("scales must be float32")
+    if weights.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"weights must be float32 or bfloat16, got {weights.dtype}")
+    if D_I != 128:
+        raise ValueError(f"D_I ({D_I}) must be 128 for quantised inputs")
+    if H_I > MAX_HEADS:
+        raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS}")
+    if top_k <= 0 or top_k > MAX_TOPK:
+        raise ValueError(f"top_k must be in [1, {MAX_TOPK}], got {top_k}")
+    if check_scales and q_scale.numel():
+        m, _ = torch.frexp(q_scale)
+        if not bool((m == 0.5).all()):
+            raise ValueError("q_scale must hold powers of two (UE8M0)")
+    ratio = 0 if causal_ratio is None else int(causal_ratio)
+    if causal_ratio is not None and ratio <= 0:
+        raise ValueError(f"causal_ratio must be a positive integer, got {causal_ratio}")
+
+    def ok(t):
+        return t.stride(-1) == 1 and all(s % 16 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+
+    q_fp4 = q_fp4 if ok(q_fp4) else q_fp4.contiguous()
+    k8 = k_fp8.view(torch.uint8)
+    k8 = k8 if ok(k8) else k8.contiguous()
+    q_scale = q_scale if q_scale.stride(-1) == 1 else q_scale.contiguous()
+    out_idx = torch.empty((B, S, top_k), dtype=torch.int64, device=q_fp4.device)
+    out_scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q_fp4.device)
+    mask_ptr, mask_strides = None, None
+    if causal_mask is not None:
+        if causal_mask.dtype != torch.bool:
+            causal_mask = causal_mask != 0
+        mask_ptr, mask_strides = causal_mask.data_ptr(), _lib.strides(causal_mask)
+    L = _lib.load()
+    with torch.cuda.device(q_fp4.device):
+        rc = L.si_indexer_topk_q(
+            q_fp4.data_ptr(), _lib.strides(q_fp4), q_scale.data_ptr(), _lib.strides(q_scale),
+            k8.data_ptr(), _lib.strides(k8), k_scale.data_ptr(), _lib.strides(k_scale),
+            weights.data_ptr(), 1 if weights.dtype == torch.bfloat16 else 0, _lib.strides(weights),
+            mask_ptr, mask_strides, B, S, T, H_I, D_I, top_k, ratio,
+            out_idx.data_ptr(), out_scores.data_ptr(), _lib.stream_ptr(q_fp4.device))
+    _lib.check(rc)
+    return out_idx, out_scores
+
+
+def chunked_indexer_topk_quantized(
+    q: torch.Tensor,
+    k_idx: torch.Tensor,
+    weights: torch.Tensor,
+    top_k: int,
+    *,
+    causal_mask: Optional[torch.Tensor] = None,
+    causal_ratio: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``chunked_indexer_topk`` under the production V4 indexer dtypes:
+    quantises bf16 ``q`` to fp4 (UE8M0 per 32 dims) and ``k_idx`` to fp8
+    (one scale per row), then runs :func:`indexer_topk_q`."""
+    from .quant import act_quant, fp4_act_quant
+
+    q4, qs = fp4_act_quant(q, 32)
+    k8, ks = act_quant(k_idx, k_idx.shape[-1])
+    return indexer_topk_q(q4, qs, k8, ks, weights, top_k, causal_mask=causal_mask, causal_ratio=causal_ratio,
+                          check_scales=False)

@@ -1,0 +1,99 @@
+"""GPU parity of the quantised-input indexer (fp4 queries, fp8 keys).
+
+The oracle scores the dequantised inputs exactly: e2m1 values times
+power-of-two scales and e4m3 values are all bf16-representable, so
+I(s, t) = k_scale[t] * oracle_indexer_scores(q_deq, k_e4m3, w) in double,
+and the GPU result goes through the same gate as the bf16 indexer
+(tests/indexer_check.py: padding, order, scores within 1e-4, exact sets
+wherever the k-th gap exceeds 1e-4 of the row scale, recall >= 0.999).
+Shapes: the reference tests' ragged ones (S=47, T=73), causal ratio 4 and an
+explicit mask, rows with no legal key, H_I = 16 / 40 / 64, top_k up to
+1024, and the quantising wrapper on bf16 inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from streamindex_amd import chunked_indexer_topk_quantized, indexer_topk_q, quant, synth
+from tests.conftest import bf16_bits
+from tests.indexer_check import check_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _dequant_bits(q4, qs, k8):
+    """bf16 bit patterns of the dequantised q and of the raw e4m3 key values."""
+    qv = O.fp4_unpack(q4.cpu().numpy()) * np.repeat(qs.cpu().numpy(), 32, axis=-1)
+    qb = O.f32_to_bf16_bits(qv.astype(np.float32))
+    assert np.array_equal(O.bf16_bits_to_f64(qb), qv), "dequantised q must be bf16-exact"
+    kv = k8.float().cpu().numpy()
+    return qb, O.f32_to_bf16_bits(kv)
+
+
+def _check(q4, qs, k8, ks, w, top_k, idx, sc, *, ratio=None, mask=None, rows=None, label=""):
+    B, S = q4.shape[:2]
+    T = k8.shape[1]
+    qb, kb = _dequant_bits(q4, qs, k8)
+    rows = np.arange(S, dtype=np.int64) if rows is None else np.asarray(rows, dtype=np.int64)
+    ksn = ks.reshape(B, T).cpu().numpy().astype(np.float64)
+    out = []
+    for b in range(B):
+        lim = O.legal_limits(rows, T, ratio)
+        ref = O.indexer_scores(qb[b], kb[b], w[b].float().cpu().numpy(), rows, lim=lim) * ksn[b][None, :]
+        mrows = None if mask is None else mask[b].cpu().numpy().astype(np.uint8)[rows]
+        out.append(check_rows(ref, lim, top_k, idx[b].cpu().numpy()[rows], sc[b].cpu().numpy()[rows], mrows,
+                              label=f"{label}[b={b}]"))
+    return out
+
+
+def _inputs(B, S, T, H, seed):
+    q, k, w = synth.indexer_inputs(B, S, H, 128, T, seed=seed)
+    q4, qs = quant.fp4_act_quant(q, 32)
+    k8, ks = quant.act_quant(k, 128)
+    return q, k, w, q4, qs, k8, ks
+
+
+@pytest.mark.parametrize("H,top_k", [(64, 64), (16, 32), (40, 200)])
+def test_causal_ratio(cuda_device, H, top_k):
+    B, S, T = 2, 600, 150
+    _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 11 + H)
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, top_k, causal_ratio=4)
+    torch.cuda.synchronize()
+    _check(q4, qs, k8, ks, w, top_k, idx, sc, ratio=4, label=f"q-ratio H{H}")
+
+
+def test_ragged_no_bound_and_mask(cuda_device):
+    # tests/test_chunked_indexer.py:51-72 shapes (S=47, T=73)
+    B, S, T, H = 1, 47, 73, 64
+    _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 5)
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, 16)
+    _check(q4, qs, k8, ks, w, 16, idx, sc, label="q-nobound")
+    g = torch.Generator().manual_seed(5)
+    mask = (torch.rand(B, S, T, generator=g) < 0.3).cuda()
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, 16, causal_mask=mask)
+    _check(q4, qs, k8, ks, w, 16, idx, sc, mask=mask, label="q-mask")
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, 128)   # top_k > T: padding
+    _check(q4, qs, k8, ks, w, 128, idx, sc, label="q-wide")
+
+
+def test_large_topk_sampled_rows(cuda_device):
+    B, S, T, H = 1, 8192, 2048, 64
+    _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 21)
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, 1024, causal_ratio=4)
+    rows = np.random.default_rng(0).choice(S, 96, replace=False)
+    rows[:3] = [0, 2, S - 1]   # no legal key, no legal key, full row
+    _check(q4, qs, k8, ks, w, 1024, idx, sc, ratio=4, rows=rows, label="q-1024")
+
+
+def test_quantising_wrapper_and_validation(cuda_device):
+    B, S, T, H = 1, 256, 64, 64
+    q, k, w, q4, qs, k8, ks = _inputs(B, S, T, H, 3)
+    idx, sc = chunked_indexer_topk_quantized(q, k, w, 32, causal_ratio=4)
+    idx2, sc2 = indexer_topk_q(q4, qs, k8, ks, w, 32, causal_ratio=4)
+    assert torch.equal(idx, idx2) and torch.equal(sc, sc2)
+    with pytest.raises(ValueError):
+        indexer_topk_q(q4, qs * 3.0, k8, ks, w, 32)   # not powers of two
+    with pytest.raises(ValueError):
+        indexer_topk_q(q4, qs, k8, ks, w, 4096)
