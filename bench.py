@@ -15,7 +15,9 @@ Printed (one JSON line, rank 0):
   peak_hbm_gib   max_memory_allocated delta during one call (inputs excluded)
   parity         recall vs the CPU oracle on sampled rows
   cpu_baseline   the CPU oracle on a bounded row sample, extrapolated
-  extra          S=1M indexer time (config[4] indexer stage), sparse-attn fwd
+  extra          S=1M indexer time (config[4] indexer stage), the indexer over
+                 the production V4 dtypes (fp4 q, fp8 k) at S=64K and 1M vs the
+                 fp8 MFMA peak with sampled-row recall, sparse-attn fwd
                  at config[3] with its HBM roofline, the sparse-attn backward
                  at config[3] (dq, dkv, dsink from the saved o / lse; sampled
                  dq rows and dkv keys against the oracle), and the end-to-end CSA
@@ -45,6 +47,7 @@ from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5033.2   # MI355X dense fp8 MFMA (the fp4 x fp8 product runs at the fp8 rate)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # Reference timings on one H200 (other hardware; context only):
 # benchmarks/results/2026-04-27/scaling_v4_flash_indexer_final.log:10,14
@@ -130,6 +133,43 @@ def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, s
     idx, sc = fn()
     torch.cuda.synchronize()
     return dict(q=q, k=k, w=w, T=T, ms=ms, wall_ms=wall, peak_gib=peak, flops=flops, idx=idx, sc=sc)
+
+
+def run_indexer_q(S, ratio, top_k, steps, warmup, H=64, D=128, seed=2026, parity_rows=256):
+    """The indexer over the production V4 dtypes: the same synthetic q / k as
+    run_indexer, quantised (untimed) to fp4 (UE8M0 per 32 dims) and fp8 (one
+    scale per key row); `indexer_topk_q` timed; sampled rows checked against the
+    oracle on the dequantised inputs (exact scores, same gate as the tests)."""
+    from oracle import oracle as O
+    from streamindex_amd import indexer_topk_q, quant
+
+    dev = torch.device("cuda:0")
+    q, k, w = synth.indexer_inputs(1, S, H, D, ratio=ratio, seed=seed, device=dev)
+    T = k.shape[1]
+    q4, qs = quant.fp4_act_quant(q, 32)
+    k8, ks = quant.act_quant(k, D)
+    del q, k
+    fn = lambda: indexer_topk_q(q4, qs, k8, ks, w, top_k, causal_ratio=ratio, check_scales=False)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
+    idx, sc = fn()
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    rows = np.sort(rng.choice(S, size=min(parity_rows, S), replace=False)).astype(np.int64)
+    sel = torch.from_numpy(rows).to(dev)
+    qv = O.fp4_unpack(q4[0, sel].cpu().numpy()) * np.repeat(qs[0, sel].cpu().numpy(), 32, axis=-1)
+    kv = k8[0].float().cpu().numpy()
+    lim = O.legal_limits(rows, T, ratio)
+    ref = O.indexer_scores(O.f32_to_bf16_bits(qv.astype(np.float32)), O.f32_to_bf16_bits(kv),
+                           w[0, sel].float().cpu().numpy(), np.arange(len(rows), dtype=np.int64), lim=lim)
+    ref = ref * ks[0, :, 0].cpu().numpy().astype(np.float64)[None, :]
+    ref_idx, _ = O.topk(ref, lim, top_k)
+    rec = O.set_overlap_recall(ref_idx, idx[0, sel].cpu().numpy())
+    flops = synth.indexer_flops(S, T, H, D, ratio)
+    return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "fp8_mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
+            "parity_rows": int(len(rows)), "recall_mean": float(rec.mean()), "recall_min": float(rec.min())}
 
 
 def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True):
@@ -293,6 +333,9 @@ def main():
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
     ap.add_argument("--only-attn", action="store_true", help="sparse-attention timing only (for profilers)")
     ap.add_argument("--only-attn-bwd", action="store_true", help="sparse-attention backward timing only (for profilers)")
+    ap.add_argument("--only-indexer-q", type=int, default=0, metavar="S",
+                    help="fp4/fp8 indexer timing only at sequence length S (for profilers)")
+    ap.add_argument("--no-indexer-q", action="store_true", help="skip the fp4/fp8 indexer measurements")
     ap.add_argument("--no-attn-bwd", action="store_true", help="skip the sparse-attention backward measurement")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end CSA forward measurements")
     ap.add_argument("--e2e-parity-rows", type=int, default=1024,
@@ -314,6 +357,10 @@ def main():
     if args.only_e2e:
         re_ = run_csa_e2e(args.only_e2e, args.steps, args.warmup, 0)
         print(json.dumps({k: v for k, v in re_.items() if not isinstance(v, dict)}), flush=True)
+        return
+    if args.only_indexer_q:
+        rq = run_indexer_q(args.only_indexer_q, args.ratio, args.top_k, args.steps, args.warmup)
+        print(json.dumps(rq), flush=True)
         return
     if args.only_attn_bwd:
         ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, bwd=True, fwd=False)
@@ -362,6 +409,12 @@ def main():
         extra["s1m_peak_hbm_gib"] = rl["peak_gib"]
         extra["reference_h200_ms_s1m"] = REF_H200_MS[1048576]
         del rl
+        torch.cuda.empty_cache()
+    if not args.no_indexer_q:
+        print("[bench] fp4/fp8 indexer S=64K and S=1M", file=sys.stderr, flush=True)
+        extra["indexer_q_s64k"] = run_indexer_q(65536, args.ratio, args.top_k, 5, 1)
+        if not args.no_long:
+            extra["indexer_q_s1m"] = run_indexer_q(1 << 20, args.ratio, args.top_k, 1, 1, parity_rows=64)
         torch.cuda.empty_cache()
     if not args.no_attn:
         print("[bench] sparse attention config[3]", file=sys.stderr, flush=True)
