@@ -110,10 +110,8 @@ struct QuantQuery {
     return s0 + s1;
   }
 
-  // Partial score (this lane's 16 heads per head block) of key nb*32 + lane%32.
-  __device__ __forceinline__ float block_score(const char* tile, int nb, int lane) const {
+  __device__ __forceinline__ void load_b(const char* tile, int nb, int lane, v8i (&kb)[KS]) const {
     const int row = nb * 32 + (lane & 31);
-    v8i kb[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + kt_off<D / 2>(row, ks * 4 + (lane >> 5)));
@@ -121,22 +119,47 @@ struct QuantQuery {
       kb[ks] = v8i{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                    static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
     }
-    float p = 0.f;
+  }
+
+  // Partial scores (this lane's 16 heads per head block) of keys lane%32 of
+  // blocks 0 and 1: the NB x HB accumulator chains are independent, so all
+  // their MFMAs issue back to back before the first epilogue reads a result.
+  template <int NBLK>
+  __device__ __forceinline__ void tile_scores(const char* tile, int lane, float& p0, float& p1) const {
+    v8i kb[NBLK][KS];
+#pragma unroll
+    for (int nb = 0; nb < NBLK; ++nb) load_b(tile, nb, lane, kb[nb]);
+    f32x16 acc[NBLK][HB];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int nb = 0; nb < NBLK; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < HB; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mb][ks], kb[nb][ks],
+                                                                         ks == 0 ? f32x16{} : acc[nb][mb], 4, 0, 0,
+                                                                         qe[mb][ks], 0, 127);
+    p0 = 0.f;
+    p1 = 0.f;
 #pragma unroll
     for (int mb = 0; mb < HB; ++mb) {
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mb][ks], kb[ks], acc, 4, 0, 0, qe[mb][ks], 0, 127);
-      p += epilogue(acc, mb);
+      p0 += epilogue(acc[0][mb], mb);
+      if constexpr (NBLK > 1) p1 += epilogue(acc[1][mb], mb);
     }
-    return p;
   }
+};
+
+// Launch shape: as the bf16 kernel (four rows, 64-key tiles) with up to three
+// workgroups per CU while the selection buffers leave room in LDS (the fp8
+// ring is half the bf16 one and the fragments use fewer VGPRs).
+template <int C>
+struct TopkQShape {
+  static constexpr int WAVES_PER_EU = C <= 1024 ? 3 : 1;
 };
 
 template <int HB, int D, int C, bool MASKED>
 __global__ __launch_bounds__(TopkShape<C>::NW * 64)
-__attribute__((amdgpu_waves_per_eu(TopkShape<C>::WAVES_PER_EU, TopkShape<C>::WAVES_PER_EU)))
+__attribute__((amdgpu_waves_per_eu(TopkQShape<C>::WAVES_PER_EU, TopkQShape<C>::WAVES_PER_EU)))
 void indexer_topk_q_kernel(IndexerQArgs a) {
   constexpr int NW = TopkShape<C>::NW;
   constexpr int NT = NW * 64;
@@ -203,8 +226,9 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
     if (nblk > 0) {
-      const float p0 = qry.block_score(tile, 0, lane);
-      const float p1 = nblk > 1 ? qry.block_score(tile, 1, lane) : 0.f;
+      float p0, p1;
+      if (nblk == NB) qry.template tile_scores<2>(tile, lane, p0, p1);
+      else qry.template tile_scores<1>(tile, lane, p0, p1);
       const SwapPair r = permlane32_swap(__float_as_uint(p0), __float_as_uint(p1));
       const float sum = (__uint_as_float(r.x) + __uint_as_float(r.y)) * kscale;
       const bool legal = t < my_lim && mok;
