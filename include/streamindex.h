@@ -186,6 +186,19 @@ int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* 
                       int64_t* out_idx, float* out_scores, void* stream);
 
 /*
+ * si_indexer_topk_q writing CSA attention index rows, as si_csa_indexer_topk
+ * does for bf16 inputs (window columns, then the picks + idx_offset, -1 past
+ * the legal count).  Replaces flash_sparse/csa.py:149-179 under the
+ * production indexer dtypes.
+ */
+int si_csa_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* q_scale,
+                          const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides,
+                          const float* k_scale, const int64_t* k_scale_strides, const void* weights, int w_dtype,
+                          const int64_t* w_strides, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                          int64_t top_k, int64_t causal_ratio, int64_t n_win, int64_t idx_offset, int32_t* out_idx,
+                          const int64_t* out_strides, float* out_scores, void* stream);
+
+/*
  * Block quantise-dequantise simulations, bit-identical to the reference formulas.
  * Replaces flash_sparse/utils/quantization.py:19-37 (fp4 = 0: act_quant_simulate,
  * fp8 e4m3, scale = amax / 448) and :40-65 (fp4 = 1: fp4_act_quant_simulate,

@@ -66,14 +66,17 @@ def _launch_hca(out: torch.Tensor, B: int, S: int, n_win: int, n_comp: int, m_pr
 
 def csa_topk_idxs(q_idx: torch.Tensor, k_idx_compressed: torch.Tensor, indexer_weights: torch.Tensor, *,
                   n_win: int, top_k: int, m: int = 4, seq_len: Optional[int] = None,
-                  return_scores: bool = False):
+                  return_scores: bool = False, quantized: bool = False):
     """Fused indexer + CSA index rows: ``[B, S, n_win + top_k]`` int32.
 
     One kernel scores every legal compressed key (``i < (s+1)//m``), keeps the
     exact top-``top_k`` per query and writes the attention index row:
     window columns first, then the picks plus ``seq_len`` (default ``S``),
     ``-1`` past the legal count.  With ``return_scores`` the picks' fp32
-    scores ``[B, S, top_k]`` (``-inf`` padded) are returned too.
+    scores ``[B, S, top_k]`` (``-inf`` padded) are returned too.  With
+    ``quantized`` the indexer runs under the production V4 dtypes: ``q_idx``
+    is quantised to fp4 (UE8M0 scale per 32 dims) and the keys to fp8 (one
+    scale per row) and scored by the fp4 x fp8 kernel (``indexer_topk_q``).
     """
     B, S, H_I, D_I, T = _check_common(q_idx, k_idx_compressed, indexer_weights)
     if top_k <= 0 or top_k > MAX_TOPK:
@@ -87,6 +90,24 @@ def csa_topk_idxs(q_idx: torch.Tensor, k_idx_compressed: torch.Tensor, indexer_w
     out = torch.empty((B, S, n_win + top_k), dtype=torch.int32, device=q_idx.device)
     scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q_idx.device) if return_scores else None
     L = _lib.load()
+    if quantized:
+        if D_I != 128 or H_I > 64:
+            raise ValueError("the quantised indexer needs D_I = 128 and H_I <= 64")
+        from .quant import act_quant, fp4_act_quant
+
+        q4, qs = fp4_act_quant(q_idx, 32)
+        k8, ks = act_quant(k_idx_compressed, D_I)
+        k8u = k8.view(torch.uint8)
+        ks = ks[..., 0].contiguous()
+        with torch.cuda.device(q_idx.device):
+            rc = L.si_csa_indexer_topk_q(
+                q4.data_ptr(), _lib.strides(q4), qs.data_ptr(), _lib.strides(qs), k8u.data_ptr(), _lib.strides(k8u),
+                ks.data_ptr(), _lib.strides(ks), indexer_weights.data_ptr(),
+                1 if indexer_weights.dtype == torch.bfloat16 else 0, _lib.strides(indexer_weights),
+                B, S, T, H_I, D_I, top_k, int(m), int(n_win), offset, out.data_ptr(), _lib.strides(out),
+                scores.data_ptr() if scores is not None else None, _lib.stream_ptr(q_idx.device))
+        _lib.check(rc)
+        return (out, scores) if return_scores else out
     with torch.cuda.device(q_idx.device):
         rc = L.si_csa_indexer_topk(
             q_idx.data_ptr(), _lib.strides(q_idx), k_idx_compressed.data_ptr(), _lib.strides(k_idx_compressed),
@@ -151,6 +172,7 @@ def flash_csa_forward(
     chunk_s: int = 1024,
     chunk_t: int = 4096,
     auto_chunk_threshold_bytes: int = 1 << 30,
+    quantized_indexer: bool = False,
 ) -> torch.Tensor:
     """End-to-end CSA forward, prefill path, one layer (``csa.py:86-207``).
 
@@ -166,6 +188,8 @@ def flash_csa_forward(
       softmax_scale: defaults to ``d ** -0.5``.
       use_triton, use_chunked_indexer, chunk_s, chunk_t, auto_chunk_threshold_bytes:
         accepted for compatibility; every setting runs the same exact HIP path.
+      quantized_indexer: select with the fp4 x fp8 indexer (the production V4
+        indexer dtypes, see :func:`csa_topk_idxs`) instead of bf16.
     Returns:
       ``o: [B, S, n_h, d]`` bf16.
     """
@@ -178,6 +202,6 @@ def flash_csa_forward(
     if int(chunk_s) <= 0 or int(chunk_t) <= 0:
         raise ValueError(f"chunk_s and chunk_t must be positive, got {chunk_s}, {chunk_t}")
     topk_idxs = csa_topk_idxs(q_idx, k_idx_compressed, indexer_weights, n_win=n_win, top_k=top_k, m=m,
-                              seq_len=S)
+                              seq_len=S, quantized=quantized_indexer)
     kv_full = torch.cat([kv, kv_compressed], dim=1)
     return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale)

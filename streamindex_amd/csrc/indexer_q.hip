@@ -51,8 +51,13 @@ struct IndexerQArgs {
   int B, S, T, H;
   int top_k;
   int ratio;
-  int64_t* out_idx;     // [B,S,top_k]
+  int64_t* out_idx;     // [B,S,top_k], or null when out_idx32 is set
   float* out_scores;    // [B,S,top_k] or null
+  // CSA index rows instead of out_idx (as IndexerArgs::out_idx32)
+  int32_t* out_idx32;
+  int64_t o32sb, o32ss;
+  int n_win;
+  int idx_offset;
 };
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -242,7 +247,15 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
 
   if (active) {
     const int64_t row = static_cast<int64_t>(b) * a.S + s;
-    TopkRowOut out{a.out_idx + row * a.top_k, a.out_scores ? a.out_scores + row * a.top_k : nullptr, nullptr, 0};
+    TopkRowOut out{nullptr, a.out_scores ? a.out_scores + row * a.top_k : nullptr, nullptr, 0};
+    if (a.out_idx32) {
+      int32_t* orow = a.out_idx32 + b * a.o32sb + static_cast<int64_t>(s) * a.o32ss;
+      write_window_cols(orow, s, a.n_win, lane);
+      out.idx32 = orow + a.n_win;
+      out.off32 = a.idx_offset;
+    } else {
+      out.idx64 = a.out_idx + row * a.top_k;
+    }
     sel.finish(out, lane);
   }
 }
@@ -273,30 +286,22 @@ static int dispatch_q(const IndexerQArgs& a, hipStream_t st) {
   return set_error(SI_ERR_UNSUPPORTED, "top_k > 2048 is not supported");
 }
 
-}  // namespace si
-
-using namespace si;
-
-extern "C" int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* q_scale,
-                                 const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides,
-                                 const float* k_scale, const int64_t* k_scale_strides, const void* weights,
-                                 int w_dtype, const int64_t* w_strides, const uint8_t* causal_mask,
-                                 const int64_t* mask_strides, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
-                                 int64_t top_k, int64_t causal_ratio, int64_t* out_idx, float* out_scores,
-                                 void* stream) {
+// Argument checks and the packed-argument fill shared by both entries.
+static int fill_q(IndexerQArgs& a, const void* q_fp4, const int64_t* q_strides, const float* q_scale,
+                  const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides, const float* k_scale,
+                  const int64_t* k_scale_strides, const void* weights, int w_dtype, const int64_t* w_strides,
+                  int64_t B, int64_t S, int64_t T, int64_t H, int64_t D, int64_t top_k, int64_t causal_ratio) {
   if (!q_strides || !q_scale_strides || !k_strides || !k_scale_strides || !w_strides)
     return set_error(SI_ERR_INVALID, "null stride argument");
   if (B < 0 || S < 0 || T < 0 || H <= 0 || D <= 0) return set_error(SI_ERR_INVALID, "negative or zero dimension");
   if (top_k <= 0) return set_error(SI_ERR_INVALID, "top_k must be positive");
   if (top_k > 2048) return set_error(SI_ERR_UNSUPPORTED, "top_k > 2048 is not supported");
-  if (causal_ratio < 0) return set_error(SI_ERR_INVALID, "causal_ratio must be >= 0");
-  if (causal_mask && causal_ratio > 0) return set_error(SI_ERR_INVALID, "causal_mask and causal_ratio are exclusive");
-  if (causal_mask && !mask_strides) return set_error(SI_ERR_INVALID, "null mask strides");
+  if (causal_ratio < 0 || causal_ratio > 0x7fffffff) return set_error(SI_ERR_INVALID, "bad causal_ratio");
   if (B > 0x7fffffff || S > 0x7fffffff || T > 0x7fffffff) return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
   if (H > 64 || D != 128)
     return set_error(SI_ERR_UNSUPPORTED, "quantised indexer supports H_I <= 64 and D_I = 128 (the V4 indexer)");
   const bool rows = B > 0 && S > 0;
-  if (rows && (!q_fp4 || !q_scale || !weights || !out_idx)) return set_error(SI_ERR_INVALID, "null pointer argument");
+  if (rows && (!q_fp4 || !q_scale || !weights)) return set_error(SI_ERR_INVALID, "null pointer argument");
   if (B > 0 && T > 0 && (!k_fp8 || !k_scale)) return set_error(SI_ERR_INVALID, "null pointer argument");
   if (q_strides[3] != 1 || k_strides[2] != 1 || q_scale_strides[3] != 1)
     return set_error(SI_ERR_INVALID, "q, q_scale and k need a contiguous last dimension");
@@ -306,7 +311,6 @@ extern "C" int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, co
     return set_error(SI_ERR_INVALID, "q / k must be 16-byte aligned");
   if (k_strides[1] >= (int64_t{1} << 24)) return set_error(SI_ERR_UNSUPPORTED, "k row stride too large");
   if (w_dtype != 0 && w_dtype != 1) return set_error(SI_ERR_INVALID, "weights dtype must be fp32 (0) or bf16 (1)");
-  IndexerQArgs a{};
   a.q = static_cast<const uint8_t*>(q_fp4);
   a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
   a.qsc = q_scale;
@@ -318,16 +322,67 @@ extern "C" int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, co
   a.w = weights;
   a.wsb = w_strides[0]; a.wss = w_strides[1]; a.wsh = w_strides[2];
   a.w_bf16 = w_dtype;
+  a.B = static_cast<int>(B); a.S = static_cast<int>(S); a.T = static_cast<int>(T); a.H = static_cast<int>(H);
+  a.top_k = static_cast<int>(top_k);
+  a.ratio = static_cast<int>(causal_ratio);
+  return SI_OK;
+}
+
+static int run_q(const IndexerQArgs& a, void* stream) {
+  if (a.B == 0 || a.S == 0) return SI_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return a.H <= 32 ? dispatch_q<1, 128>(a, st) : dispatch_q<2, 128>(a, st);
+}
+
+}  // namespace si
+
+using namespace si;
+
+extern "C" int si_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* q_scale,
+                                 const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides,
+                                 const float* k_scale, const int64_t* k_scale_strides, const void* weights,
+                                 int w_dtype, const int64_t* w_strides, const uint8_t* causal_mask,
+                                 const int64_t* mask_strides, int64_t B, int64_t S, int64_t T, int64_t H, int64_t D,
+                                 int64_t top_k, int64_t causal_ratio, int64_t* out_idx, float* out_scores,
+                                 void* stream) {
+  IndexerQArgs a{};
+  int rc = fill_q(a, q_fp4, q_strides, q_scale, q_scale_strides, k_fp8, k_strides, k_scale, k_scale_strides, weights,
+                  w_dtype, w_strides, B, S, T, H, D, top_k, causal_ratio);
+  if (rc) return rc;
+  if (causal_mask && causal_ratio > 0) return set_error(SI_ERR_INVALID, "causal_mask and causal_ratio are exclusive");
+  if (causal_mask && !mask_strides) return set_error(SI_ERR_INVALID, "null mask strides");
+  if (B > 0 && S > 0 && !out_idx) return set_error(SI_ERR_INVALID, "null output pointer");
   a.mask = causal_mask;
   if (causal_mask) {
     a.msb = mask_strides[0]; a.mss = mask_strides[1]; a.mst = mask_strides[2];
   }
-  a.B = static_cast<int>(B); a.S = static_cast<int>(S); a.T = static_cast<int>(T); a.H = static_cast<int>(H);
-  a.top_k = static_cast<int>(top_k);
-  a.ratio = static_cast<int>(causal_ratio);
   a.out_idx = out_idx;
   a.out_scores = out_scores;
-  if (!rows) return SI_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  return H <= 32 ? dispatch_q<1, 128>(a, st) : dispatch_q<2, 128>(a, st);
+  return run_q(a, stream);
+}
+
+extern "C" int si_csa_indexer_topk_q(const void* q_fp4, const int64_t* q_strides, const float* q_scale,
+                                     const int64_t* q_scale_strides, const void* k_fp8, const int64_t* k_strides,
+                                     const float* k_scale, const int64_t* k_scale_strides, const void* weights,
+                                     int w_dtype, const int64_t* w_strides, int64_t B, int64_t S, int64_t T,
+                                     int64_t H, int64_t D, int64_t top_k, int64_t causal_ratio, int64_t n_win,
+                                     int64_t idx_offset, int32_t* out_idx, const int64_t* out_strides,
+                                     float* out_scores, void* stream) {
+  IndexerQArgs a{};
+  int rc = fill_q(a, q_fp4, q_strides, q_scale, q_scale_strides, k_fp8, k_strides, k_scale, k_scale_strides, weights,
+                  w_dtype, w_strides, B, S, T, H, D, top_k, causal_ratio);
+  if (rc) return rc;
+  if (n_win < 0 || n_win > 0x7fffffff) return set_error(SI_ERR_INVALID, "n_win must be non-negative");
+  if (idx_offset < 0 || idx_offset + T > 0x7fffffff)
+    return set_error(SI_ERR_UNSUPPORTED, "idx_offset + T must fit in int32");
+  if (!out_strides) return set_error(SI_ERR_INVALID, "null output strides");
+  if (!out_idx && B > 0 && S > 0) return set_error(SI_ERR_INVALID, "null output pointer");
+  if (out_strides[2] != 1) return set_error(SI_ERR_INVALID, "index rows must be contiguous");
+  a.out_scores = out_scores;
+  a.out_idx32 = out_idx;
+  a.o32sb = out_strides[0];
+  a.o32ss = out_strides[1];
+  a.n_win = static_cast<int>(n_win);
+  a.idx_offset = static_cast<int>(idx_offset);
+  return run_q(a, stream);
 }

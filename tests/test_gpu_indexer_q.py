@@ -97,3 +97,25 @@ def test_quantising_wrapper_and_validation(cuda_device):
         indexer_topk_q(q4, qs * 3.0, k8, ks, w, 32)   # not powers of two
     with pytest.raises(ValueError):
         indexer_topk_q(q4, qs, k8, ks, w, 4096)
+
+
+def test_csa_rows_and_forward_quantized(cuda_device):
+    from streamindex_amd import csa_topk_idxs, flash_csa_forward, sparse_attn
+
+    B, S, H, n_win, top_k, m = 1, 512, 64, 32, 48, 4
+    T = S // m
+    _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 17)
+    q, k, _ = synth.indexer_inputs(B, S, H, 128, T, seed=17)
+    rows, sc = csa_topk_idxs(q, k, w, n_win=n_win, top_k=top_k, m=m, return_scores=True, quantized=True)
+    torch.cuda.synchronize()
+    ref_win = O.window_idxs(np.arange(S, dtype=np.int64), n_win)
+    assert np.array_equal(rows[0, :, :n_win].cpu().numpy(), ref_win)
+    picks = rows[..., n_win:].long()
+    picks = torch.where(picks >= 0, picks - S, picks)
+    _check(q4, qs, k8, ks, w, top_k, picks, sc, ratio=m, label="csa-q")
+    # the forward over those rows equals sparse attention over [kv ; kv_compressed]
+    qa, kv, sink = synth.sparse_attn_inputs(B, S, 16, 64, S, seed=18)
+    kvc = kv[:, :T].contiguous()
+    o = flash_csa_forward(qa, kv, kvc, q, k, w, sink, n_win=n_win, top_k=top_k, m=m, quantized_indexer=True)
+    o2 = sparse_attn(qa, torch.cat([kv, kvc], 1), sink, rows)
+    assert torch.equal(o, o2)
