@@ -24,7 +24,9 @@ Printed (one JSON line, rank 0):
                  forward (flash_csa_forward: fused indexer -> int32 window +
                  compressed index rows -> sparse attention, 64 heads, d=576,
                  n_win=128) at S=64K and at S=1M (config[4]) with its stage
-                 split, peak HBM and sampled-row recall against the oracle
+                 split, peak HBM and sampled-row recall against the oracle,
+                 and at S=1M again with the fp4/fp8 indexer (the production
+                 V4 indexer dtypes, quantised inside the timed call)
 """
 
 from __future__ import annotations
@@ -275,12 +277,16 @@ def csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=8, seed=4):
     return float(np.abs(o[0].float().cpu().numpy() - ro).max())
 
 
-def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m=4, n_win=128, top_k=512):
-    """flash_csa_forward at V4-Flash dims; returns timings, stage split, peak HBM and parity."""
+def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m=4, n_win=128, top_k=512,
+                quantized=False):
+    """flash_csa_forward at V4-Flash dims; returns timings, stage split, peak HBM and parity.  With
+    ``quantized`` the indexer runs under the production dtypes (fp4 q, fp8 k, quantised inside the
+    timed call); the recall is then that of the quantised selection against the bf16 oracle."""
     dev = torch.device("cuda:0")
     qi, ki, w = synth.indexer_inputs(1, S, H_I, D_I, ratio=m, seed=2026, device=dev)
     q, kv, kvc, sink = synth.csa_attn_inputs(1, S, n_h, d, S // m, seed=2027, device=dev)
-    fn = lambda: flash_csa_forward(q, kv, kvc, qi, ki, w, sink, n_win=n_win, top_k=top_k, m=m)  # noqa: E731
+    fn = lambda: flash_csa_forward(q, kv, kvc, qi, ki, w, sink, n_win=n_win, top_k=top_k, m=m,  # noqa: E731
+                                   quantized_indexer=quantized)
     for _ in range(max(1, warmup)):
         fn()
     torch.cuda.synchronize()
@@ -290,7 +296,7 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     # stage split of one call (same three steps flash_csa_forward runs)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     ev[0].record(stream)
-    rows_gpu = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m, seq_len=S)
+    rows_gpu = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m, seq_len=S, quantized=quantized)
     ev[1].record(stream)
     kv_full = torch.cat([kv, kvc], dim=1)
     ev[2].record(stream)
@@ -310,7 +316,8 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     res["indexer_tflops"] = res["indexer_flops"] / (res["indexer_ms"] * 1e-3) / 1e12
     res["attn_tflops"] = res["attn_flops"] / (res["attn_ms"] * 1e-3) / 1e12
     if parity_rows > 0:
-        res["parity"] = csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m, parity_rows)
+        res["recall_vs_bf16_oracle" if quantized else "parity"] = csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m,
+                                                                            parity_rows)
         res["attn_max_abs_err"] = csa_attn_check(q, kv, kvc, sink, rows_gpu)
     del q, kv, kvc, qi, ki, w, rows_gpu
     torch.cuda.empty_cache()
@@ -436,6 +443,8 @@ def main():
         extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256)
         print("[bench] end-to-end CSA forward S=1M (config[4])", file=sys.stderr, flush=True)
         extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
+        print("[bench] end-to-end CSA forward S=1M with the fp4/fp8 indexer", file=sys.stderr, flush=True)
+        extra["csa_e2e_s1m_quantized_indexer"] = run_csa_e2e(1 << 20, 1, 1, 256, quantized=True)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
