@@ -168,6 +168,20 @@ int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, 
                        void* stream);
 
 /*
+ * Inverted top-k index.  Replaces flash_sparse/triton/inverted_topk.py:75-128
+ * (build_inverted_topk).
+ *   topk_idxs [B,S,K] int32 / int64 (strides in elements); keys outside [0, n_kv) ignored.
+ *   inv_count [B,n_kv] int32: pairs selecting each key (not clamped);
+ *   inv_topk [B,n_kv,k_max] int32: their query indices in ascending (query, slot)
+ *   order, -1 past min(count, k_max).
+ *   workspace: si_build_inverted_topk_workspace_bytes(B, S, K, n_kv) bytes.
+ */
+int64_t si_build_inverted_topk_workspace_bytes(int64_t B, int64_t S, int64_t K, int64_t n_kv);
+int si_build_inverted_topk(const void* topk_idxs, int idx_is_i64, const int64_t* idx_strides, int64_t B, int64_t S,
+                           int64_t K, int64_t n_kv, int64_t k_max, int32_t* inv_topk, int32_t* inv_count,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Indexer + exact top-k over quantised inputs (the production V4 indexer
  * dtypes: fp4 queries, fp8 keys).  Same operator as si_indexer_topk
  * (flash_sparse/triton/chunked_indexer.py:47-160) on the dequantised values

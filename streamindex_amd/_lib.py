@@ -49,6 +49,8 @@ SIGNATURES = {
                                  _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "si_csa_indexer_topk_q": (_I32, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I32, _I64P,
                                      _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P, _P]),
+    "si_build_inverted_topk_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "si_build_inverted_topk": (_I32, [_P, _I32, _I64P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "si_quant_simulate": (_I32, [_P, _P, _I32, _I64, _I64, _I32, _P]),
     "si_quant_pack": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I32, _I32, _P]),
     "si_token_compress": (_I32, [_P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P]),

@@ -910,6 +910,57 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
   return check_launch("sparse_attn_bwd_dsink_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// inverted top-k index (flash_sparse/triton/inverted_topk.py:75-128)
+// ---------------------------------------------------------------------------
+// For key id b N + t: inv_count = its number of (query, slot) pairs, and the
+// first min(count, k_max) entries of its inv_topk row the queries of those
+// pairs in ascending (query, slot) order (the stable sort's order); the
+// remaining entries are -1.
+__global__ void inverted_fill_kernel(const uint32_t* pair, const int32_t* lo, const int32_t* hi, int64_t nkeys,
+                                     int S, int K, int k_max, int32_t* inv_topk, int32_t* inv_count) {
+  const int64_t kid = blockIdx.x;
+  if (kid >= nkeys) return;
+  const int a = lo[kid], c = hi[kid] - lo[kid];
+  if (threadIdx.x == 0) inv_count[kid] = c;
+  int32_t* row = inv_topk + kid * k_max;
+  for (int j = threadIdx.x; j < k_max; j += blockDim.x)
+    row[j] = j < c ? static_cast<int32_t>((pair[a + j] / static_cast<uint32_t>(K)) % static_cast<uint32_t>(S)) : -1;
+}
+
+struct InvPlan {
+  size_t seg_lo, seg_hi, kin, kout, vin, vout, tmp, tmp_bytes, total;
+};
+
+static int inv_plan(int64_t B, int64_t S, int64_t K, int64_t N, InvPlan* p) {
+  const int64_t nkeys = B * N;
+  const size_t npairs = static_cast<size_t>(B) * S * K;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = bwd_align(off + bytes);
+    return at;
+  };
+  p->seg_lo = take(static_cast<size_t>(nkeys) * 4);
+  p->seg_hi = take(static_cast<size_t>(nkeys) * 4);
+  p->kin = take(npairs * 4);
+  p->kout = take(npairs * 4);
+  p->vin = take(npairs * 4);
+  p->vout = take(npairs * 4);
+  size_t tmp = 0;
+  if (npairs > 0) {
+    const hipError_t e = rocprim::radix_sort_pairs(nullptr, tmp, static_cast<uint32_t*>(nullptr),
+                                                   static_cast<uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
+                                                   static_cast<uint32_t*>(nullptr), npairs, 0u, bwd_end_bit(nkeys),
+                                                   static_cast<hipStream_t>(0));
+    if (e != hipSuccess) return set_error(SI_ERR_LAUNCH, std::string("radix sort size query: ") + hipGetErrorString(e));
+  }
+  p->tmp_bytes = tmp;
+  p->tmp = take(tmp);
+  p->total = off;
+  return SI_OK;
+}
+
 static bool bwd_supported_d(int64_t D) {
   return D == 32 || D == 64 || D == 128 || D == 256 || D == 512 || D == 576;
 }
@@ -1019,4 +1070,68 @@ extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const
     case 512: return launch_bwd<512>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
     default: return launch_bwd<576>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
   }
+}
+
+static int inv_check(int64_t B, int64_t S, int64_t K, int64_t N, int64_t k_max) {
+  if (B < 0 || S < 0 || K < 0 || N < 0 || k_max < 0) return set_error(SI_ERR_INVALID, "bad dimension");
+  if (B * N >= (int64_t{1} << 31) || B * S * K >= (int64_t{1} << 32) || S > 0x7fffffff || K > 0x7fffffff ||
+      N * k_max >= (int64_t{1} << 40))
+    return set_error(SI_ERR_UNSUPPORTED, "inverted index too large");
+  return SI_OK;
+}
+
+extern "C" int64_t si_build_inverted_topk_workspace_bytes(int64_t B, int64_t S, int64_t K, int64_t n_kv) {
+  if (inv_check(B, S, K, n_kv, 0)) return -1;
+  InvPlan p{};
+  if (inv_plan(B, S, K, n_kv, &p)) return -1;
+  return static_cast<int64_t>(p.total);
+}
+
+extern "C" int si_build_inverted_topk(const void* topk_idxs, int idx_is_i64, const int64_t* idx_strides, int64_t B,
+                                      int64_t S, int64_t K, int64_t n_kv, int64_t k_max, int32_t* inv_topk,
+                                      int32_t* inv_count, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = inv_check(B, S, K, n_kv, k_max);
+  if (rc) return rc;
+  if (!idx_strides) return set_error(SI_ERR_INVALID, "null stride argument");
+  const int64_t nkeys = B * n_kv;
+  const int64_t npairs = B * S * K;
+  if ((npairs > 0 && !topk_idxs) || (nkeys > 0 && (!inv_count || (k_max > 0 && !inv_topk))))
+    return set_error(SI_ERR_INVALID, "null pointer argument");
+  InvPlan pl{};
+  if ((rc = inv_plan(B, S, K, n_kv, &pl))) return rc;
+  if (static_cast<int64_t>(pl.total) > workspace_bytes || (pl.total > 0 && !workspace))
+    return set_error(SI_ERR_INVALID, "workspace too small (see si_build_inverted_topk_workspace_bytes)");
+  if (nkeys == 0) return SI_OK;
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint32_t* kin = reinterpret_cast<uint32_t*>(ws + pl.kin);
+  uint32_t* kout = reinterpret_cast<uint32_t*>(ws + pl.kout);
+  uint32_t* vin = reinterpret_cast<uint32_t*>(ws + pl.vin);
+  uint32_t* vout = reinterpret_cast<uint32_t*>(ws + pl.vout);
+  int32_t* seg_lo = reinterpret_cast<int32_t*>(ws + pl.seg_lo);
+  int32_t* seg_hi = reinterpret_cast<int32_t*>(ws + pl.seg_hi);
+  const int64_t fblocks = (nkeys + 255) / 256 < 65536 ? (nkeys + 255) / 256 : 65536;
+  hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_lo,
+                     nkeys, 0);
+  hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_hi,
+                     nkeys, 0);
+  if ((rc = check_launch("sparse_attn_bwd_fill_kernel"))) return rc;
+  if (npairs > 0) {
+    const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
+    hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, topk_idxs, idx_is_i64 ? 1 : 0,
+                       idx_strides[0], idx_strides[1], idx_strides[2], static_cast<int>(S), static_cast<int>(n_kv),
+                       static_cast<int>(K), int64_t{0}, npairs, static_cast<uint32_t>(nkeys), kin, vin);
+    if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
+    size_t tmp_bytes = pl.tmp_bytes;
+    const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,
+                                                   static_cast<size_t>(npairs), 0u, bwd_end_bit(nkeys), st);
+    if (e != hipSuccess) return set_error(SI_ERR_LAUNCH, std::string("radix sort: ") + hipGetErrorString(e));
+    hipLaunchKernelGGL(sparse_attn_bwd_segments_kernel, dim3(pblocks), dim3(256), 0, st, kout, npairs,
+                       static_cast<uint32_t>(nkeys), seg_lo, seg_hi);
+    if ((rc = check_launch("sparse_attn_bwd_segments_kernel"))) return rc;
+  }
+  hipLaunchKernelGGL(inverted_fill_kernel, dim3(static_cast<unsigned>(nkeys)), dim3(64), 0, st, vout, seg_lo, seg_hi,
+                     nkeys, static_cast<int>(S > 0 ? S : 1), static_cast<int>(K > 0 ? K : 1),
+                     static_cast<int>(k_max), inv_topk, inv_count);
+  return check_launch("inverted_fill_kernel");
 }

@@ -175,6 +175,51 @@ def sparse_attn_bwd(
     return dq, dkv, dsink
 
 
+def sparse_attn_bwd_v2(q, kv, attn_sink, topk_idxs, o, lse, do, softmax_scale: Optional[float] = None, *,
+                       block_h: Optional[int] = None, block_n: int = 64, block_q: int = 8,
+                       k_max: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The reference's atomic-free backward variant (``sparse_attn_bwd_v2.py:381-416``).
+
+    :func:`sparse_attn_bwd` already reduces dkv key by key without atomics (the
+    idea v2 prototypes), so this is the same computation; the tiling knobs are
+    accepted and ignored, and there is no ``k_max`` bound on the queries per key.
+    """
+    del block_h, block_n, block_q, k_max
+    return sparse_attn_bwd(q, kv, attn_sink, topk_idxs, o, lse, do, softmax_scale)
+
+
+def build_inverted_topk(topk_idxs: torch.Tensor, n_kv: int, k_max: int, *, block_k: int = 64
+                        ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Inverted top-k index (``flash_sparse/triton/inverted_topk.py:75-128``).
+
+    Returns ``(inv_topk [B, n_kv, k_max] int32, inv_count [B, n_kv] int32)``:
+    ``inv_count[b, t]`` is the number of (query, slot) entries selecting key
+    ``t`` (not clamped to ``k_max``), and the first ``min(count, k_max)``
+    entries of ``inv_topk[b, t]`` are their query indices in ascending
+    (query, slot) order (the reference leaves the order to its atomics); the
+    rest are ``-1``.  Indices outside ``[0, n_kv)`` are ignored.
+    """
+    del block_k
+    assert topk_idxs.is_cuda and topk_idxs.dim() == 3
+    B, S, K = topk_idxs.shape
+    if topk_idxs.dtype not in (torch.int32, torch.int64):
+        topk_idxs = topk_idxs.to(torch.int64)
+    inv_topk = torch.empty((B, n_kv, k_max), dtype=torch.int32, device=topk_idxs.device)
+    inv_count = torch.empty((B, n_kv), dtype=torch.int32, device=topk_idxs.device)
+    L = _lib.load()
+    with torch.cuda.device(topk_idxs.device):
+        need = L.si_build_inverted_topk_workspace_bytes(B, S, K, n_kv)
+        if need < 0:
+            raise ValueError(L.si_last_error().decode("utf-8", "replace"))
+        ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=topk_idxs.device)
+        rc = L.si_build_inverted_topk(topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0,
+                                      _lib.strides(topk_idxs), B, S, K, n_kv, k_max, inv_topk.data_ptr(),
+                                      inv_count.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      _lib.stream_ptr(topk_idxs.device))
+    _lib.check(rc)
+    return inv_topk, inv_count
+
+
 class _SparseAttnFunc(torch.autograd.Function):
     """``flash_sparse/triton/__init__.py:19-44``: saves q, kv, attn_sink,
     topk_idxs, o and lse for the backward."""
@@ -198,4 +243,4 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = No
     return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale)
 
 
-__all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn"]
+__all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn_bwd_v2", "sparse_attn", "build_inverted_topk"]

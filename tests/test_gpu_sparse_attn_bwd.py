@@ -201,3 +201,52 @@ def test_bwd_v4_shape_sampled(cuda_device):
     _close(dq[0, rows].float().cpu().numpy(), rdq[0], "v4 dq rows")
     _close(dkv[0, keys].float().cpu().numpy(), rdkv[0], "v4 dkv keys")
     assert np.all(np.abs(dsink.cpu().numpy() - rds) <= _dsink_bound(o, do, sink, lse))
+
+
+def test_inverted_topk_correctness(cuda_device):
+    # tests/test_inverted_topk.py:18-67 (distinct picks per query, every 4th slot masked)
+    from streamindex_amd import build_inverted_topk
+
+    B, S, K, N, K_MAX = 2, 32, 8, 64, 32
+    g = torch.Generator().manual_seed(600)
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B * S)]).reshape(B, S, K).int()
+    idx[:, :, ::4] = -1
+    idx[0, 3, 1] = N + 5   # out of range: ignored
+    inv, cnt = build_inverted_topk(idx.cuda(), n_kv=N, k_max=K_MAX)
+    inv, cnt = inv.cpu().numpy(), cnt.cpu().numpy()
+    ic = idx.numpy()
+    for b in range(B):
+        for t in range(N):
+            qs = [s for s in range(S) for j in range(K) if ic[b, s, j] == t]
+            assert cnt[b, t] == len(qs)
+            assert list(inv[b, t, :len(qs)]) == qs          # ascending (query, slot) order
+            assert np.all(inv[b, t, len(qs):] == -1)
+
+
+def test_inverted_topk_counts_overflow(cuda_device):
+    # tests/test_inverted_topk.py:70-95: counts are not clamped to k_max
+    from streamindex_amd import build_inverted_topk
+
+    B, S, K, N, K_MAX = 1, 64, 4, 16, 8
+    g = torch.Generator().manual_seed(601)
+    idx = torch.zeros((B, S, K), dtype=torch.int32)
+    idx[:, :, 1:] = torch.randint(1, N, (B, S, K - 1), generator=g, dtype=torch.int32)
+    inv, cnt = build_inverted_topk(idx.cuda(), n_kv=N, k_max=K_MAX)
+    assert cnt[0, 0].item() == 64
+    assert list(inv[0, 0].cpu().numpy()) == list(range(K_MAX))
+
+
+def test_bwd_v2_matches_v1(cuda_device):
+    # tests/test_triton_sparse_attn_bwd_v2.py:46-100 (including H > 64)
+    from streamindex_amd import sparse_attn_bwd_v2
+
+    for (H, seed) in [(16, 700), (128, 702)]:
+        q, kv, sink, idx, do = _inputs(1, 32, H, 64, 64, 16, seed)
+        o, lse = sparse_attn_fwd(q, kv, sink, idx)
+        a = sparse_attn_bwd(q, kv, sink, idx, o, lse, do)
+        b = sparse_attn_bwd_v2(q, kv, sink, idx, o, lse, do, block_q=4, k_max=8)
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+        rdq, rdkv, _ = _oracle(q, kv, sink, idx, o, lse, do, 64 ** -0.5)
+        _close(b[0][0].float().cpu().numpy(), rdq[0], f"v2 dq H{H}")
+        _close(b[1][0].float().cpu().numpy(), rdkv[0], f"v2 dkv H{H}")
