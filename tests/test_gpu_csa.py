@@ -215,3 +215,48 @@ def test_flash_hca_forward_matches_oracle(cuda_device, B, S, n_h, d, mp, n_win, 
     err = np.abs(got - o_ref).max()
     assert err <= 2e-2, f"max |o - o_ref| = {err}"
     assert _norm_corr(torch.from_numpy(got), torch.from_numpy(o_ref)) < 5e-3
+
+
+def _grad_check(fwd, q, kv, kvc, sink, rows, do, label):
+    """Gradients of a CSA / HCA forward through autograd against the oracle
+    backward over the same index rows and [kv ; kv_compressed] (the selection
+    itself is not differentiable, as in the reference)."""
+    from oracle import oracle as O
+    from streamindex_amd import sparse_attn_fwd
+
+    qr, kvr, kvcr, sr = (t.clone().requires_grad_(True) for t in (q, kv, kvc, sink))
+    o = fwd(qr, kvr, kvcr, sr)
+    o.backward(do)
+    S = q.shape[1]
+    kv_full = torch.cat([kv, kvc], 1)
+    o2, lse = sparse_attn_fwd(q, kv_full, sink, rows)
+    assert torch.equal(o.detach(), o2)
+    bits = lambda t: t[0].cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    rdq, rdkv, rds = O.sparse_attn_bwd_rows(bits(q), bits(kv_full), bits(o2), bits(do), sink.cpu().numpy(),
+                                            lse[0].cpu().numpy(), rows[0].cpu().numpy().astype(np.int64),
+                                            q.shape[-1] ** -0.5)
+    for name, got, ref in (("dq", qr.grad[0], rdq), ("dkv", kvr.grad[0], rdkv[:S]), ("dkv_c", kvcr.grad[0], rdkv[S:])):
+        g = got.float().cpu().numpy()
+        assert np.linalg.norm(g - ref) <= 1e-2 * np.linalg.norm(ref) + 1e-6, f"{label} {name}"
+    assert np.abs(sr.grad.cpu().numpy() - rds).max() <= 1e-3 * max(1.0, np.abs(rds).max()), f"{label} dsink"
+
+
+def test_csa_and_hca_backward(cuda_device):
+    # the intent of tests/test_gradient_check.py:7-14 (CSA / HCA backward), checked
+    # against the oracle instead of torch.autograd.gradcheck (bf16 inputs)
+    from streamindex_amd import build_hca_topk_idxs, csa_topk_idxs, flash_csa_forward, flash_hca_forward
+
+    B, S, n_h, d, m, n_win, top_k = 1, 256, 16, 64, 4, 16, 24
+    T = S // m
+    qi, ki, w = synth.indexer_inputs(B, S, 64, 128, T, seed=31)
+    q, kv, kvc, sink = synth.csa_attn_inputs(B, S, n_h, d, T, seed=32, scale=0.5)
+    g = torch.Generator().manual_seed(33)
+    do = (torch.randn(B, S, n_h, d, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    rows = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m)
+    _grad_check(lambda a, b, c, s: flash_csa_forward(a, b, c, qi, ki, w, s, n_win=n_win, top_k=top_k, m=m),
+                q, kv, kvc, sink, rows, do, "csa")
+    mp = 16
+    kvc_h = kvc[:, :S // mp].contiguous()
+    rows_h = build_hca_topk_idxs(B=B, seq_len=S, n_win=n_win, n_compressed=S // mp, m_prime=mp, device=q.device)
+    _grad_check(lambda a, b, c, s: flash_hca_forward(a, b, c, s, n_win=n_win, m_prime=mp), q, kv, kvc_h, sink,
+                rows_h.int(), do, "hca")
