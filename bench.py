@@ -43,8 +43,8 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from streamindex_amd import (chunked_indexer_topk, csa_topk_idxs, flash_csa_forward, sparse_attn,  # noqa: E402
-                             sparse_attn_bwd, sparse_attn_fwd)
+from streamindex_amd import (build_hca_topk_idxs, chunked_indexer_topk, csa_topk_idxs,  # noqa: E402
+                             flash_csa_forward, flash_hca_forward, sparse_attn, sparse_attn_bwd, sparse_attn_fwd)
 from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
 
@@ -324,6 +324,47 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     return res
 
 
+def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=128):
+    """flash_hca_forward at V4-Flash attention dims (window n_win plus every causally legal
+    compressed entry, ratio m_prime; ``hca.py:54-95``).  The index rows end in the masked
+    compressed tail, on average half the row: whole 32-key tiles of it are skipped by the
+    attention kernel.  Returns timings, stage split, useful FLOPs and parity on sampled rows."""
+    dev = torch.device("cuda:0")
+    T = S // m_prime
+    q, kv, kvc, sink = synth.csa_attn_inputs(1, S, n_h, d, T, seed=2029, device=dev)
+    fn = lambda: flash_hca_forward(q, kv, kvc, sink, n_win=n_win, m_prime=m_prime)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ms = _events_time(fn, steps, stream)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record(stream)
+    rows_gpu = build_hca_topk_idxs(B=1, seq_len=S, n_win=n_win, n_compressed=T, m_prime=m_prime, device=dev)
+    ev[1].record(stream)
+    kv_full = torch.cat([kv, kvc], dim=1)
+    ev[2].record(stream)
+    o = sparse_attn(q, kv_full, sink, rows_gpu, None)
+    ev[3].record(stream)
+    torch.cuda.synchronize()
+    del o, kv_full
+    nvalid = float((rows_gpu >= 0).sum().item())
+    K = n_win + T
+    res = {
+        "S": S, "T": T, "n_h": n_h, "d": d, "n_win": n_win, "m_prime": m_prime, "K": K, "ms": ms,
+        "rows_ms": ev[0].elapsed_time(ev[1]), "concat_ms": ev[1].elapsed_time(ev[2]),
+        "attn_ms": ev[2].elapsed_time(ev[3]),
+        "valid_frac": nvalid / (S * K),
+        "attn_flops": 4.0 * n_h * d * nvalid,
+    }
+    res["attn_tflops"] = res["attn_flops"] / (res["attn_ms"] * 1e-3) / 1e12
+    if check_rows > 0:
+        res["attn_max_abs_err"] = csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=check_rows)
+    del q, kv, kvc, rows_gpu
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -349,6 +390,8 @@ def main():
                     help="sampled rows for the S=1M end-to-end recall check (config[4] asks 1024)")
     ap.add_argument("--only-e2e", type=int, default=0, metavar="S",
                     help="end-to-end CSA forward timing at sequence length S only (for profilers)")
+    ap.add_argument("--only-hca", type=int, default=0, metavar="S",
+                    help="end-to-end HCA forward timing at sequence length S only (for profilers)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run 5 plain device copies of MIB MiB (scales HBM byte counters) and exit")
     args = ap.parse_args()
@@ -360,6 +403,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_mib": args.calibrate_copy, "launches": 5}), flush=True)
+        return
+    if args.only_hca:
+        rh = run_hca_e2e(args.only_hca, args.steps, args.warmup, 0)
+        print(json.dumps(rh), flush=True)
         return
     if args.only_e2e:
         re_ = run_csa_e2e(args.only_e2e, args.steps, args.warmup, 0)
@@ -445,6 +492,8 @@ def main():
         extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
         print("[bench] end-to-end CSA forward S=1M with the fp4/fp8 indexer", file=sys.stderr, flush=True)
         extra["csa_e2e_s1m_quantized_indexer"] = run_csa_e2e(1 << 20, 1, 1, 256, quantized=True)
+        print("[bench] end-to-end HCA forward S=64K", file=sys.stderr, flush=True)
+        extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

@@ -28,7 +28,8 @@ Deliberate differences (documented for drop-in users):
   every setting yields the same indices.
 * Ties among equal scores rank the smaller compressed index first
   (``torch.topk`` leaves tie order unspecified).
-* The result is forward-only (``sparse_attn`` raises on backward).
+* Gradients flow through ``sparse_attn``'s autograd (the HIP backward) into
+  ``q``, ``kv`` / ``kv_compressed`` and ``attn_sink``; the index rows carry none.
 """
 
 from __future__ import annotations

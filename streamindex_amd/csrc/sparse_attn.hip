@@ -86,6 +86,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   __shared__ __attribute__((aligned(16))) char kv_lds[SH::LDS_KV];
   __shared__ __attribute__((aligned(16))) char p_lds[2][kAttnWaves * 64 * 16];  // P^T B-fragments per head block
   __shared__ float alpha_lds[2][64];
+  __shared__ int live_lds[2];  // tile has at least one valid key (published with alpha)
   __shared__ float scale_lds[64];
   __shared__ __attribute__((aligned(16))) float bias_lds[kAttnRing][kAttnTK];  // 0: key used, -inf: masked
   __shared__ uint32_t rowoff_lds[kAttnRing][kAttnTK];    // offset of the key's KV row, 16-byte units
@@ -255,12 +256,16 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
     // (inline asm: the compiler makes a tracked LDS access that follows
     // LDS-DMA copies wait for all of them; the tile barrier's lgkmcnt(0)
     // orders these stores)
-    auto softmax_store = [&](int t, const SoftmaxOut& r) {
+    auto softmax_store = [&](int t, const SoftmaxOut& r, bool live) {
       const uint32_t pa = lds_addr(&p_lds[t & 1][(wave * 64 + lane) * 16]);
       asm volatile("ds_write_b128 %0, %1" ::"v"(pa), "v"(r.w) : "memory");
       if (g == 0) {
         const uint32_t aa = lds_addr(reinterpret_cast<const char*>(&alpha_lds[t & 1][wave * 16 + i16]));
         asm volatile("ds_write_b32 %0, %1" ::"v"(aa), "v"(r.alpha) : "memory");
+      }
+      if (wave == 0 && lane == 0) {
+        const uint32_t la = lds_addr(reinterpret_cast<const char*>(&live_lds[t & 1]));
+        asm volatile("ds_write_b32 %0, %1" ::"v"(la), "v"(live ? 1 : 0) : "memory");
       }
     };
     // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r);
@@ -269,6 +274,16 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
       bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
     };
+    // Whether any key of the tile is valid (wave-uniform): the four lane
+    // groups' biases cover all 32 keys.  An all-masked tile needs no S^T (its
+    // scores are 0 + bias = -inf either way) and no P.V (P = 0).
+    auto tile_live = [&](const f32x4 (&bias)[2]) {
+      bool any = false;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) any |= (bias[0][r] == 0.f) | (bias[1][r] == 0.f);
+      return __builtin_amdgcn_ballot_w64(any) != 0;
+    };
+    const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (ntiles > 0) {
       __syncthreads();  // indices of tiles 0..3 published
@@ -282,12 +297,13 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       __syncthreads();  // tile 0 landed
       f32x4 bias_cur[2];
       {
-        f32x4 bias[2], st[2];
+        f32x4 bias[2], st[2] = {zero4, zero4};
         read_bias(0, bias);
         read_bias(1, bias_cur);
         read_roff(3, roff);
-        qk(0, st);
-        softmax_store(0, softmax(st, bias));
+        const bool live = tile_live(bias);
+        if (live) qk(0, st);
+        softmax_store(0, softmax(st, bias), live);
       }
       // tile 1 landed; the copies of tile 2 may still be in flight
       if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
@@ -304,9 +320,10 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         read_roff(it + 4, roff_nx);
         if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
         if (it + 1 < ntiles) {
-          f32x4 st[2];
-          qk(it + 1, st);
-          softmax_store(it + 1, softmax(st, bias_cur));
+          f32x4 st[2] = {zero4, zero4};
+          const bool live = tile_live(bias_cur);
+          if (live) qk(it + 1, st);
+          softmax_store(it + 1, softmax(st, bias_cur), live);
         }
         bias_cur[0] = bias_nx[0];
         bias_cur[1] = bias_nx[1];
@@ -433,6 +450,9 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       float al[4];
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+      // wave-uniform in a scalar register, so the skip is a scalar branch
+      // (MFMAs do not honour EXEC)
+      const bool live = __builtin_amdgcn_readfirstlane(live_lds[it & 1]) != 0;
       if (idx_wave && it + 6 < ntiles) load_idx(it + 6);
       const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
                                                            al[3] != 1.0f) != 0;
@@ -442,7 +462,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
 #pragma unroll
           for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
       }
-      pv(it);
+      if (live) pv(it);  // P = 0 for a tile without a valid key
       // the indices of tile it+5 (copied one iteration ago) landed; in the
       // index wave those of tile it+6 may stay in flight
       if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(1));

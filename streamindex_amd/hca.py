@@ -9,7 +9,7 @@ sparse-attention kernel as CSA.  The index rows are written by one HIP kernel
 arange/where/cat passes.
 
 ``use_triton`` is accepted for compatibility and selects nothing (one HIP
-implementation).  Forward-only.
+implementation).  Gradients flow through ``sparse_attn``'s autograd.
 """
 
 from __future__ import annotations

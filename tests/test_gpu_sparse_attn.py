@@ -94,6 +94,37 @@ def test_masking_equals_truncation(cuda_device):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+@pytest.mark.parametrize("D,i64", [(576, False), (128, True), (512, False)])
+def test_fully_masked_tiles(cuda_device, D, i64):
+    # Whole 32-key tiles of -1 (the first tile, tiles in the middle, the last
+    # one, every tile of some rows) as HCA's causal tail produces them: the
+    # result equals the oracle and, bit for bit, the same rows with those
+    # tiles removed.
+    B, S, H, N, K = 1, 16, 64, 400, 256
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=600 + D, q_scale=0.5, kv_scale=0.5)
+    g = torch.Generator().manual_seed(D)
+    dt = torch.int64 if i64 else torch.int32
+    idx = torch.randint(0, N, (B, S, K), generator=g, dtype=dt)
+    dead = [0, 3, 4, 7]
+    for t in dead:
+        idx[:, :, 32 * t:32 * t + 32] = -1
+    idx[:, 5, :] = -1                  # every tile masked
+    idx[:, 6, 32 * 5 + 7] = 17         # one valid key in an otherwise dead row
+    idx[:, 6, :32 * 5 + 7] = -1
+    idx[:, 6, 32 * 5 + 8:] = -1
+    idx = idx.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, D ** -0.5)
+    torch.cuda.synchronize()
+    _check(q, kv, sink, idx, D ** -0.5, o, lse, f"dead tiles D={D}")
+    assert o[:, 5].float().abs().max().item() == 0.0
+    keep = torch.tensor([t for t in range(K // 32) if t not in dead])
+    cols = (keep.view(-1, 1) * 32 + torch.arange(32)).flatten().cuda()
+    rows = [r for r in range(S) if r not in (5, 6)]
+    o2, l2 = sparse_attn_fwd(q[:, rows], kv, sink, idx[:, rows][:, :, cols].contiguous(), D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:, rows], o2) and torch.equal(lse[:, rows], l2)
+
+
 @pytest.mark.parametrize("D", [32, 64, 128, 256, 512, 576])
 def test_head_dims(cuda_device, D):
     B, S, H, N, K = 1, 24, 64, 300, 96
