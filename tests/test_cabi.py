@@ -191,6 +191,22 @@ def test_reference_import_paths():
     assert chunked_indexer_topk is si.chunked_indexer_topk
     assert indexer_score is si.indexer_score and indexer_score_topk is si.indexer_score_topk
     assert sparse_attn_fwd is si.sparse_attn_fwd and ft.sparse_attn is si.sparse_attn
+    assert ft.sparse_attn_fwd is si.sparse_attn_fwd   # still the function after the submodule import
+
+    from flash_sparse.triton.sparse_attn_bwd import sparse_attn_bwd
+    from flash_sparse.triton.sparse_attn_bwd_v2 import sparse_attn_bwd_v2
+    from flash_sparse.triton.inverted_topk import build_inverted_topk
+    from flash_sparse.triton.indexer_streaming_topk import streaming_indexer_topk
+    from flash_sparse.utils.quantization import act_quant_simulate, fp4_act_quant_simulate
+    from flash_sparse.utils.compression import softmax_gated_pool
+
+    assert ft.sparse_attn_bwd is sparse_attn_bwd is si.sparse_attn_bwd
+    assert sparse_attn_bwd_v2 is si.sparse_attn_bwd_v2 and build_inverted_topk is si.build_inverted_topk
+    from streamindex_amd import compressor, quant
+
+    assert act_quant_simulate is quant.act_quant_simulate and fp4_act_quant_simulate is quant.fp4_act_quant_simulate
+    assert softmax_gated_pool is compressor.softmax_gated_pool
+    assert callable(streaming_indexer_topk)
 
 
 def test_synth_legal_pairs_closed_form():
