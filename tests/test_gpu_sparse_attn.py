@@ -125,6 +125,42 @@ def test_fully_masked_tiles(cuda_device, D, i64):
     assert torch.equal(o[:, rows], o2) and torch.equal(lse[:, rows], l2)
 
 
+@pytest.mark.parametrize("D,H,B,S,K,i64", [(576, 64, 1, 700, 32, False), (576, 64, 2, 600, 96, True),
+                                           (576, 80, 1, 400, 64, False), (128, 16, 1, 1000, 200, False),
+                                           (512, 128, 1, 300, 160, True)])
+def test_many_rows_per_workgroup(cuda_device, D, H, B, S, K, i64):
+    # More query rows than compute units, with 1, 3, 2, 7 and 5 key tiles per
+    # row, two head groups (full and partial), H < 64, B = 2 and int64
+    # indices.  Sampled rows (first, last and spread) against the oracle; some
+    # rows fully masked.
+    N = 300
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=700 + D + H, q_scale=0.5, kv_scale=0.5)
+    g = torch.Generator().manual_seed(S + K)
+    idx = torch.randint(-1, N, (B, S, K), generator=g, dtype=torch.int64 if i64 else torch.int32)
+    idx[:, 3::17, :] = -1
+    idx = idx.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, D ** -0.5)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, S, max(1, S // 23)), [0, 1, 3, S - 2, S - 1]]))
+    rows = rows[rows < S]
+    for b in range(B):
+        sel = torch.from_numpy(rows).cuda()
+        ro, rl = O.sparse_attn_rows(bf16_bits(q[b, sel]), bf16_bits(kv[b]), sink.cpu().numpy(),
+                                    idx[b, sel].cpu().numpy().astype(np.int64), D ** -0.5)
+        go = o[b, sel].float().cpu().numpy()
+        gl = lse[b, sel].cpu().numpy()
+        assert np.isfinite(go).all()
+        assert np.abs(go - ro).max() <= O_TOL, f"b={b}: o error {np.abs(go - ro).max():.3e}"
+        assert np.abs(gl - rl).max() <= LSE_TOL * max(1.0, np.abs(rl).max())
+    # a slice of the rows launched on its own: identical bits (a row's result
+    # does not depend on the other rows of the launch)
+    lo = 256 if S >= 296 else S // 2
+    hi = min(S, lo + 40)
+    o2, l2 = sparse_attn_fwd(q[:, lo:hi].contiguous(), kv, sink, idx[:, lo:hi].contiguous(), D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:, lo:hi], o2) and torch.equal(lse[:, lo:hi], l2)
+
+
 @pytest.mark.parametrize("D", [32, 64, 128, 256, 512, 576])
 def test_head_dims(cuda_device, D):
     B, S, H, N, K = 1, 24, 64, 300, 96
