@@ -496,12 +496,20 @@ def main():
         extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8)
 
     traffic = None
+    tfile = {}
     if os.path.exists(TRAFFIC_FILE):
         try:
             with open(TRAFFIC_FILE) as f:
-                traffic = json.load(f).get("indexer_topk_c1_bytes_per_launch")
+                tfile = json.load(f)
+            traffic = tfile.get("indexer_topk_c1_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    if "sparse_attn_ms" in extra and tfile.get("sparse_attn_c3_bytes_per_launch"):
+        # fabric bytes per launch (HBM byte counters: L2-missing gathers, q, o, indices) over the
+        # measured time: the bound of this kernel on random indices
+        fab = tfile["sparse_attn_c3_bytes_per_launch"] / (extra["sparse_attn_ms"] * 1e-3) / 1e9
+        extra["sparse_attn_fabric_gbps"] = fab
+        extra["sparse_attn_fabric_frac"] = fab / PEAK_HBM_GBPS
 
     line = {
         "metric": "V4-Flash indexer ms @S=64K/1M, MFMA util %, peak HBM GB (1 GPU)",

@@ -812,10 +812,17 @@ static int bwd_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64
 }
 
 // Largest chunk (query rows) whose plan fits `bytes`; 0 when even one row does not.
+// A chunk also keeps its (query, slot) pairs and its grid (rows x head groups)
+// inside int32: sort keys, payloads and segment bounds are 32-bit.
 static int bwd_rows_for(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64_t K, size_t bytes, BwdPlan* out) {
-  const int64_t total = B * S;
+  const int64_t HG = (H + 63) / 64;
+  int64_t total = B * S;
   BwdPlan p{};
   if (total <= 0) return bwd_plan(B, S, H, D, N, K, 0, out);
+  const int64_t kLim = 0x7fffffff;
+  int64_t cap = kLim / (K > 0 ? K : 1);
+  if (kLim / HG < cap) cap = kLim / HG;
+  if (total > cap) total = cap;
   int rc = bwd_plan(B, S, H, D, N, K, total, &p);
   if (rc) return rc;
   if (p.total <= bytes) {
@@ -1074,7 +1081,8 @@ extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const
 
 static int inv_check(int64_t B, int64_t S, int64_t K, int64_t N, int64_t k_max) {
   if (B < 0 || S < 0 || K < 0 || N < 0 || k_max < 0) return set_error(SI_ERR_INVALID, "bad dimension");
-  if (B * N >= (int64_t{1} << 31) || B * S * K >= (int64_t{1} << 32) || S > 0x7fffffff || K > 0x7fffffff ||
+  // pair positions (segment bounds) are int32
+  if (B * N >= (int64_t{1} << 31) || B * S * K >= (int64_t{1} << 31) || S > 0x7fffffff || K > 0x7fffffff ||
       N * k_max >= (int64_t{1} << 40))
     return set_error(SI_ERR_UNSUPPORTED, "inverted index too large");
   return SI_OK;

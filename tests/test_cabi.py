@@ -131,6 +131,16 @@ def test_csa_hca_validation_codes_without_gpu(lib):
     assert rc == _lib.SI_OK
 
 
+def test_backward_and_inverted_index_limits_without_gpu(lib):
+    # sizes whose (query, slot) pair positions would not fit the int32 segment bounds
+    assert lib.si_build_inverted_topk_workspace_bytes(1, 1 << 21, 1 << 10, 4096) == -1
+    assert b"too large" in lib.si_last_error()
+    assert lib.si_sparse_attn_bwd_workspace_bytes(1, 1 << 31, 64, 576, 4096, 512, 1 << 30) == -1
+    assert b"int32" in lib.si_last_error()
+    assert lib.si_sparse_attn_bwd_workspace_bytes(1, 16, 64, 100, 64, 8, 1 << 30) == -1
+    assert b"D=100" in lib.si_last_error()
+
+
 def test_python_layer_errors_on_cpu_tensors():
     from streamindex_amd import chunked_indexer_topk, indexer_score, sparse_attn_fwd
 

@@ -128,7 +128,7 @@ def test_fully_masked_tiles(cuda_device, D, i64):
 @pytest.mark.parametrize("D,H,B,S,K,i64", [(576, 64, 1, 700, 32, False), (576, 64, 2, 600, 96, True),
                                            (576, 80, 1, 400, 64, False), (128, 16, 1, 1000, 200, False),
                                            (512, 128, 1, 300, 160, True)])
-def test_many_rows_per_workgroup(cuda_device, D, H, B, S, K, i64):
+def test_many_rows(cuda_device, D, H, B, S, K, i64):
     # More query rows than compute units, with 1, 3, 2, 7 and 5 key tiles per
     # row, two head groups (full and partial), H < 64, B = 2 and int64
     # indices.  Sampled rows (first, last and spread) against the oracle; some
