@@ -5,9 +5,9 @@ eq. 11-12 for CSA with two overlapping streams, eq. 22-23 for HCA) and
 ``flash_sparse/utils/compression.py:13-24`` (``softmax_gated_pool``).  The
 kernels compute in fp32 and round the result to the input dtype once (the
 reference's torch ops round after each step in bf16).  The mounted reference
-builds the overlap path only inside its bias-shape error branch (the
-indentation pattern of SURVEY Appendix A); the function-level behaviour its
-docstring states is implemented.
+builds the overlap path only inside its bias-shape error branch (its body is
+indented one level too deep, ``flash_sparse/reference.py:230-270``); the
+function-level behaviour its docstring states is implemented.
 """
 
 from __future__ import annotations
