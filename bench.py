@@ -47,6 +47,8 @@ from streamindex_amd import (build_hca_topk_idxs, chunked_indexer_topk, csa_topk
                              flash_csa_forward, flash_hca_forward, sparse_attn, sparse_attn_bwd, sparse_attn_fwd)
 from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
+from streamindex_amd.csa import csa_row_len  # noqa: E402
+from streamindex_amd.hca import hca_row_len  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5033.2   # MI355X dense fp8 MFMA (the fp4 x fp8 product runs at the fp8 rate)
@@ -297,10 +299,11 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     ev[0].record(stream)
     rows_gpu = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m, seq_len=S, quantized=quantized)
+    row_len = csa_row_len(1, S, n_win, top_k, S // m, m, dev)
     ev[1].record(stream)
     kv_full = torch.cat([kv, kvc], dim=1)
     ev[2].record(stream)
-    o = sparse_attn(q, kv_full, sink, rows_gpu, None)
+    o = sparse_attn(q, kv_full, sink, rows_gpu, None, row_len=row_len)
     ev[3].record(stream)
     torch.cuda.synchronize()
     del o, kv_full
@@ -341,10 +344,11 @@ def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     ev[0].record(stream)
     rows_gpu = build_hca_topk_idxs(B=1, seq_len=S, n_win=n_win, n_compressed=T, m_prime=m_prime, device=dev)
+    row_len = hca_row_len(1, S, n_win, T, m_prime, dev)
     ev[1].record(stream)
     kv_full = torch.cat([kv, kvc], dim=1)
     ev[2].record(stream)
-    o = sparse_attn(q, kv_full, sink, rows_gpu, None)
+    o = sparse_attn(q, kv_full, sink, rows_gpu, None, row_len=row_len)
     ev[3].record(stream)
     torch.cuda.synchronize()
     del o, kv_full

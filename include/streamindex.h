@@ -93,6 +93,21 @@ int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, 
                        const int64_t* lse_strides, void* stream);
 
 /*
+ * si_sparse_attn_fwd with optional per-row column counts: row_len [B,S]
+ * int32 (strides in elements); columns j >= row_len[b,s] are masked and the
+ * 32-key tiles past it are never gathered or computed.  row_len = NULL is
+ * si_sparse_attn_fwd.  No counterpart in the reference (whose HCA rows,
+ * flash_sparse/hca.py:40-51, carry a -1 tail of known length through
+ * sparse_attn_fwd.py:180-292); used by the HCA / CSA compositions.
+ */
+int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                              const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                              const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D, int64_t N_kv,
+                              int64_t K, float softmax_scale, void* o, const int64_t* o_strides, float* lse,
+                              const int64_t* lse_strides, const int32_t* row_len, const int64_t* row_len_strides,
+                              void* stream);
+
+/*
  * Fused indexer top-k that writes CSA attention index rows directly.
  * Replaces flash_sparse/csa.py:149-179 (chunked indexer, window indices,
  * "+S" offset of the compressed picks, int32 concat) and, for the same

@@ -42,7 +42,7 @@ from . import _lib
 from .indexer import _check_common, _prep, MAX_TOPK
 from .sparse_attn import sparse_attn
 
-__all__ = ["flash_csa_forward", "build_csa_topk_idxs", "csa_topk_idxs", "build_sliding_window_idxs"]
+__all__ = ["flash_csa_forward", "build_csa_topk_idxs", "csa_topk_idxs", "build_sliding_window_idxs", "csa_row_len"]
 
 
 def build_sliding_window_idxs(B: int, S: int, n_win: int, device) -> torch.Tensor:
@@ -205,4 +205,14 @@ def flash_csa_forward(
     topk_idxs = csa_topk_idxs(q_idx, k_idx_compressed, indexer_weights, n_win=n_win, top_k=top_k, m=m,
                               seq_len=S, quantized=quantized_indexer)
     kv_full = torch.cat([kv, kv_compressed], dim=1)
-    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale)
+    row_len = csa_row_len(B, S, n_win, top_k, n_compressed, m, q.device)
+    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+
+
+def csa_row_len(B: int, S: int, n_win: int, top_k: int, n_compressed: int, m: int, device) -> torch.Tensor:
+    """``[B, S]`` int32 used columns of the fused CSA rows: the window, then
+    ``min(top_k, n_compressed, (s+1)//m)`` picks (every legal key has a finite
+    score, so a row holds that many); the ``-1`` rest is never run."""
+    s = torch.arange(S, device=device)
+    legal = torch.clamp((s + 1) // m, max=n_compressed)
+    return (n_win + torch.clamp(legal, max=top_k)).to(torch.int32).expand(B, S)

@@ -62,6 +62,8 @@ struct SparseAttnArgs {
   float* lse;          // [B,S,H]
   int64_t lsb, lss, lsh;
   int B, S, H, N, K;
+  const int32_t* row_len;  // optional [B,S]: columns at or past row_len[b,s] are masked (tiles past it skipped)
+  int64_t rlsb, rlss;
   int HG;              // head groups of 64
   float scale_log2;    // softmax_scale * log2(e)
 };
@@ -105,8 +107,15 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   const int b = rest % a.B;
   const int hg = rest / a.B;
   const int hbase = hg * 64;
-  // with no KV rows every key is masked: the tile loop is skipped
-  const int ntiles = a.N > 0 ? (a.K + kAttnTK - 1) / kAttnTK : 0;
+  // Columns of this row: K, or fewer when a row length is given (the rest
+  // are masked and their tiles never run).  With no KV rows every key is
+  // masked: the tile loop is skipped.
+  int klen = a.K;
+  if (a.row_len) {
+    const int rl = a.row_len[b * a.rlsb + static_cast<int64_t>(s) * a.rlss];
+    klen = rl < 0 ? 0 : (rl < a.K ? rl : a.K);
+  }
+  const int ntiles = a.N > 0 ? (klen + kAttnTK - 1) / kAttnTK : 0;
 
   // Tile protocol (one barrier per tile).  Iteration `it`: the consumers
   // compute P.V of tile it while the producers compute S^T + softmax of tile
@@ -375,7 +384,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
     auto load_idx = [&](int t) {
       // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
       int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
-      j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
+      j = j < klen ? j : klen - 1;  // klen > 0 whenever a tile exists
       const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
                                        (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
@@ -388,7 +397,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
                                                          idxraw_lds[rslot][2 * lane])
                                   : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
         const int j = t * kAttnTK + lane;
-        const bool ok = j < a.K && raw >= 0 && raw < a.N;
+        const bool ok = j < klen && raw >= 0 && raw < a.N;
         bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
         rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
       }
@@ -540,11 +549,13 @@ static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
 
 using namespace si;
 
-extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
-                                  const float* attn_sink, const void* topk_idxs, int idx_is_i64,
-                                  const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D,
-                                  int64_t N_kv, int64_t K, float softmax_scale, void* o, const int64_t* o_strides,
-                                  float* lse, const int64_t* lse_strides, void* stream) {
+extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv,
+                                         const int64_t* kv_strides, const float* attn_sink, const void* topk_idxs,
+                                         int idx_is_i64, const int64_t* idx_strides, int64_t B, int64_t S, int64_t H,
+                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* o,
+                                         const int64_t* o_strides, float* lse, const int64_t* lse_strides,
+                                         const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
+  if (row_len && !row_len_strides) return set_error(SI_ERR_INVALID, "null row_len strides");
   if (!q_strides || !kv_strides || !idx_strides || !o_strides || !lse_strides)
     return set_error(SI_ERR_INVALID, "null stride argument");
   if (B < 0 || S < 0 || H <= 0 || D <= 0 || N_kv < 0 || K < 0) return set_error(SI_ERR_INVALID, "bad dimension");
@@ -581,6 +592,11 @@ extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const
   a.lsb = lse_strides[0]; a.lss = lse_strides[1]; a.lsh = lse_strides[2];
   a.B = static_cast<int>(B); a.S = static_cast<int>(S); a.H = static_cast<int>(H);
   a.N = static_cast<int>(N_kv); a.K = static_cast<int>(K);
+  a.row_len = row_len;
+  if (row_len) {
+    a.rlsb = row_len_strides[0];
+    a.rlss = row_len_strides[1];
+  }
   a.HG = static_cast<int>((H + 63) / 64);
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   if (a.B == 0 || a.S == 0) return SI_OK;
@@ -596,4 +612,14 @@ extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const
       return set_error(SI_ERR_UNSUPPORTED,
                        "unsupported head dim D=" + std::to_string(D) + " (supported: 32, 64, 128, 256, 512, 576)");
   }
+}
+
+extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                                  const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                                  const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D,
+                                  int64_t N_kv, int64_t K, float softmax_scale, void* o, const int64_t* o_strides,
+                                  float* lse, const int64_t* lse_strides, void* stream) {
+  return si_sparse_attn_fwd_ragged(q, q_strides, kv, kv_strides, attn_sink, topk_idxs, idx_is_i64, idx_strides, B, S,
+                                   H, D, N_kv, K, softmax_scale, o, o_strides, lse, lse_strides, nullptr, nullptr,
+                                   stream);
 }

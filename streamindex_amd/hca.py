@@ -21,7 +21,7 @@ import torch
 from .csa import _launch_hca
 from .sparse_attn import sparse_attn
 
-__all__ = ["flash_hca_forward", "build_hca_topk_idxs"]
+__all__ = ["flash_hca_forward", "build_hca_topk_idxs", "hca_row_len"]
 
 
 def build_hca_topk_idxs(*, B: int, seq_len: int, n_win: int, n_compressed: int, m_prime: int,
@@ -68,4 +68,13 @@ def flash_hca_forward(
     topk_idxs = build_hca_topk_idxs(B=B, seq_len=S, n_win=n_win, n_compressed=n_compressed, m_prime=m_prime,
                                     device=q.device)
     kv_full = torch.cat([kv, kv_compressed], dim=1)
-    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale)
+    row_len = hca_row_len(B, S, n_win, n_compressed, m_prime, q.device)
+    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+
+
+def hca_row_len(B: int, S: int, n_win: int, n_compressed: int, m_prime: int, device) -> torch.Tensor:
+    """``[B, S]`` int32 used columns of the HCA rows: the window, then the
+    ``min(n_compressed, (s+1)//m_prime)`` legal compressed entries; the rest
+    of each row is ``-1``, so attention never runs those tiles."""
+    s = torch.arange(S, device=device)
+    return (n_win + torch.clamp((s + 1) // m_prime, max=n_compressed)).to(torch.int32).expand(B, S)

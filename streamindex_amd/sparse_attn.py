@@ -41,6 +41,7 @@ def sparse_attn_fwd(
     *,
     block_h: Optional[int] = None,
     block_n: int = 64,
+    row_len: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """MQA sparse attention with attention sink.
 
@@ -48,6 +49,10 @@ def sparse_attn_fwd(
       q: ``[B, S, H, D]`` bf16.  kv: ``[B, N_kv, D]`` bf16 (one shared head).
       attn_sink: ``[H]`` fp32.  topk_idxs: ``[B, S, K]`` int32/int64, ``-1`` = masked.
       softmax_scale: defaults to ``D ** -0.5``.
+      row_len: optional ``[B, S]`` int32 (an extension, not in the reference):
+        columns ``j >= row_len[b, s]`` are masked and their 32-key tiles are
+        never gathered or computed.  For rows whose tail is already ``-1``
+        (HCA, short CSA rows) the result is unchanged and the tail costs nothing.
     Returns:
       ``(o [B,S,H,D] bf16, lse [B,S,H] fp32)``.  A row with no valid index
       gets ``o = 0`` and ``lse = sink`` (or ``-1e30`` if the sink is ``-inf``).
@@ -84,15 +89,20 @@ def sparse_attn_fwd(
     if not ok(kv):
         kv = kv.contiguous()
     attn_sink = attn_sink.contiguous()
+    if row_len is not None:
+        assert row_len.is_cuda and row_len.shape == (B, S), "row_len must be [B, S] on the GPU"
+        if row_len.dtype != torch.int32:
+            row_len = row_len.to(torch.int32)
     o = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, S, H), dtype=torch.float32, device=q.device)
     L = _lib.load()
     with torch.cuda.device(q.device):
-        rc = L.si_sparse_attn_fwd(
+        rc = L.si_sparse_attn_fwd_ragged(
             q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
             topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
             B, S, H, D, N_kv, K, float(softmax_scale), o.data_ptr(), _lib.strides(o),
-            lse.data_ptr(), _lib.strides(lse), _lib.stream_ptr(q.device))
+            lse.data_ptr(), _lib.strides(lse), None if row_len is None else row_len.data_ptr(),
+            None if row_len is None else _lib.strides(row_len), _lib.stream_ptr(q.device))
     _lib.check(rc)
     return o, lse
 
@@ -225,22 +235,28 @@ class _SparseAttnFunc(torch.autograd.Function):
     topk_idxs, o and lse for the backward."""
 
     @staticmethod
-    def forward(ctx, q, kv, attn_sink, topk_idxs, softmax_scale):
-        o, lse = sparse_attn_fwd(q, kv, attn_sink, topk_idxs, softmax_scale)
-        ctx.save_for_backward(q, kv, attn_sink, topk_idxs, o, lse)
+    def forward(ctx, q, kv, attn_sink, topk_idxs, softmax_scale, row_len):
+        o, lse = sparse_attn_fwd(q, kv, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+        ctx.save_for_backward(q, kv, attn_sink, topk_idxs, o, lse, row_len)
         ctx.softmax_scale = softmax_scale
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, kv, attn_sink, topk_idxs, o, lse = ctx.saved_tensors
+        q, kv, attn_sink, topk_idxs, o, lse, row_len = ctx.saved_tensors
+        if row_len is not None:
+            # the forward treated columns past row_len as masked: so does the backward
+            col = torch.arange(topk_idxs.shape[-1], device=topk_idxs.device)
+            topk_idxs = topk_idxs.masked_fill(col >= row_len.unsqueeze(-1).long(), -1)
         dq, dkv, dsink = sparse_attn_bwd(q, kv, attn_sink, topk_idxs, o, lse, do.contiguous(), ctx.softmax_scale)
-        return dq, dkv, dsink, None, None
+        return dq, dkv, dsink, None, None, None
 
 
-def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = None) -> torch.Tensor:
-    """Differentiable sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``)."""
-    return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale)
+def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = None, *,
+                row_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Differentiable sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``).
+    ``row_len`` as in :func:`sparse_attn_fwd` (an extension)."""
+    return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale, row_len)
 
 
 __all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn_bwd_v2", "sparse_attn", "build_inverted_topk"]

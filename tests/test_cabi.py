@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.si_abi_version() == 4
+    assert lib.si_abi_version() == 5
     assert lib.si_indexer_topk_workspace_bytes(1, 1 << 20, 1 << 18, 64, 128, 512) == 0
 
 

@@ -161,6 +161,30 @@ def test_many_rows(cuda_device, D, H, B, S, K, i64):
     assert torch.equal(o[:, lo:hi], o2) and torch.equal(lse[:, lo:hi], l2)
 
 
+@pytest.mark.parametrize("D,i64", [(576, False), (128, True)])
+def test_row_len(cuda_device, D, i64):
+    # Per-row column counts (0, inside a tile, on a tile edge, past K, random):
+    # columns at or past row_len are masked and their tiles never run.  Equal
+    # to the oracle over the tail-masked rows, and bit for bit to the plain
+    # forward over those rows (whose dead tiles are skipped, not dropped).
+    B, S, H, N, K = 2, 40, 64, 300, 200
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=800 + D, q_scale=0.5, kv_scale=0.5)
+    g = torch.Generator().manual_seed(D)
+    idx = torch.randint(-1, N, (B, S, K), generator=g, dtype=torch.int64 if i64 else torch.int32)
+    rl = torch.randint(0, K + 40, (B, S), generator=g, dtype=torch.int32)
+    rl[:, :6] = torch.tensor([0, 1, 31, 32, 33, K], dtype=torch.int32)
+    rl[:, 6] = K + 7
+    idx, rl = idx.cuda(), rl.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, D ** -0.5, row_len=rl)
+    col = torch.arange(K, device="cuda")
+    masked = idx.masked_fill(col >= rl.unsqueeze(-1).long(), -1)
+    o2, l2 = sparse_attn_fwd(q, kv, sink, masked, D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, l2)
+    _check(q, kv, sink, masked, D ** -0.5, o, lse, f"row_len D={D}")
+    assert o[:, 0].float().abs().max().item() == 0.0  # row_len 0: nothing attended
+
+
 @pytest.mark.parametrize("D", [32, 64, 128, 256, 512, 576])
 def test_head_dims(cuda_device, D):
     B, S, H, N, K = 1, 24, 64, 300, 96
