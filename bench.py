@@ -327,7 +327,7 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     return res
 
 
-def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=128):
+def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=128, bwd=False):
     """flash_hca_forward at V4-Flash attention dims (window n_win plus every causally legal
     compressed entry, ratio m_prime; ``hca.py:54-95``).  The index rows end in the masked
     compressed tail, on average half the row: whole 32-key tiles of it are skipped by the
@@ -364,6 +364,22 @@ def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=
     res["attn_tflops"] = res["attn_flops"] / (res["attn_ms"] * 1e-3) / 1e12
     if check_rows > 0:
         res["attn_max_abs_err"] = csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=check_rows)
+    if bwd:
+        # backward of the whole composition through autograd (the index rows carry no gradient)
+        qg, kvg, kvcg, sg = (t.detach().requires_grad_() for t in (q, kv, kvc, sink))
+        og = flash_hca_forward(qg, kvg, kvcg, sg, n_win=n_win, m_prime=m_prime)
+        do = torch.randn_like(og)
+        og.backward(do, retain_graph=True)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            og.backward(do, retain_graph=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res["bwd_ms"] = e0.elapsed_time(e1) / steps
+        res["bwd_tflops"] = 10.0 * n_h * d * nvalid / (res["bwd_ms"] * 1e-3) / 1e12
+        del qg, kvg, kvcg, sg, og, do
     del q, kv, kvc, rows_gpu
     torch.cuda.empty_cache()
     return res
@@ -409,7 +425,7 @@ def main():
         print(json.dumps({"copy_mib": args.calibrate_copy, "launches": 5}), flush=True)
         return
     if args.only_hca:
-        rh = run_hca_e2e(args.only_hca, args.steps, args.warmup, 0)
+        rh = run_hca_e2e(args.only_hca, args.steps, args.warmup, 0, bwd=not args.no_attn_bwd)
         print(json.dumps(rh), flush=True)
         return
     if args.only_e2e:
@@ -497,7 +513,7 @@ def main():
         print("[bench] end-to-end CSA forward S=1M with the fp4/fp8 indexer", file=sys.stderr, flush=True)
         extra["csa_e2e_s1m_quantized_indexer"] = run_csa_e2e(1 << 20, 1, 1, 256, quantized=True)
         print("[bench] end-to-end HCA forward S=64K", file=sys.stderr, flush=True)
-        extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8)
+        extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8, bwd=not args.no_attn_bwd)
 
     traffic = None
     tfile = {}

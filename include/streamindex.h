@@ -183,6 +183,22 @@ int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, 
                        void* stream);
 
 /*
+ * si_sparse_attn_bwd with optional per-row column counts, as
+ * si_sparse_attn_fwd_ragged: row_len [B,S] int32 (strides in elements);
+ * columns j >= row_len[b,s] are masked and their tiles are skipped.  No
+ * counterpart in the reference; the backward of the HCA / CSA compositions.
+ * The workspace is sized as for si_sparse_attn_bwd.
+ */
+int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                              const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                              const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
+                              const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
+                              int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
+                              const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides, float* dsink,
+                              void* workspace, int64_t workspace_bytes, const int32_t* row_len,
+                              const int64_t* row_len_strides, void* stream);
+
+/*
  * Inverted top-k index.  Replaces flash_sparse/triton/inverted_topk.py:75-128
  * (build_inverted_topk).
  *   topk_idxs [B,S,K] int32 / int64 (strides in elements); keys outside [0, n_kv) ignored.

@@ -62,6 +62,9 @@ SIGNATURES = {
     "si_sparse_attn_bwd": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                                   _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
                                   _P, _I64P, _P, _I64P, _P, _P, _I64, _P]),
+    "si_sparse_attn_bwd_ragged": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                                         _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                         _P, _I64P, _P, _I64P, _P, _P, _I64, _P, _I64P, _P]),
 }
 
 

@@ -66,13 +66,22 @@ struct AttnBwdArgs {
   float* dsink_rows;   // [B*S, 64*HG]: -e^{sink-lse} delta per (row, head)
   uint16_t* coef;      // [nrows, HG, ntiles, 2, 4, 64, 8] bf16: P, dS fragments
   uint16_t* prow;      // [nrows, HG, 32 ntiles, D] bf16: per-(query, slot) dkv rows
-  int B, S, H, N, K, HG, ntiles;
+  int B, S, H, N, K, HG, ntiles;  // ntiles: key tiles of a full row (the workspace layout)
+  const int32_t* row_len;  // optional [B,S]: columns at or past row_len[b,s] are masked, their tiles skipped
+  int64_t rlsb, rlss;
   int64_t row0;        // first global row (b*S + s) of this chunk
   int nrows;           // rows in this chunk
   float scale, scale_log2;
 };
 
 constexpr int kBwdThreads = 2 * kAttnWaves * 64;
+
+// Columns of row (b, s): K, or fewer when row lengths are given.
+__device__ __forceinline__ int bwd_row_len(const AttnBwdArgs& a, int b, int s) {
+  if (!a.row_len) return a.K;
+  const int rl = a.row_len[b * a.rlsb + static_cast<int64_t>(s) * a.rlss];
+  return rl < 0 ? 0 : (rl < a.K ? rl : a.K);
+}
 // bf16 elements of one tile's coefficient block: [P, dS][wave][lane][8 keys]
 constexpr int kCoefTile = 2 * kAttnWaves * 64 * 8;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -109,7 +118,8 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
   const int b = static_cast<int>(grow / a.S);
   const int s = static_cast<int>(grow % a.S);
   const int hbase = hg * 64;
-  const int ntiles = a.ntiles;
+  const int klen = bwd_row_len(a, b, s);
+  const int ntiles = a.ntiles > 0 ? (klen + kAttnTK - 1) / kAttnTK : 0;  // tiles of this row
 
   // Tile protocol (one barrier per tile), as in the forward kernel: in
   // iteration `it` the consumers accumulate dQ of tile it while the
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
       mfma_result_fence(dp[0], dp[1]);
     };
 
-    uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * ntiles * kCoefTile;
+    uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * a.ntiles * kCoefTile;
     // P and dS of tile t for head hq: dS^T goes to LDS for the dQ waves, both
     // to the coefficient workspace, as bf16 B-fragments whose k-slots
     // 8g+0..3 / 8g+4..7 hold keys 4g+0..3 / 16+4g+0..3.
@@ -268,7 +278,7 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
     // ring slot t % 4.
     auto load_idx = [&](int t) {
       int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
-      j = j < a.K ? j : a.K - 1;  // a.K > 0 whenever a tile exists
+      j = j < klen ? j : klen - 1;  // klen > 0 whenever a tile exists
       const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
                                        (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
@@ -281,7 +291,7 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
                                                          idxraw_lds[rslot][2 * lane])
                                   : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
         const int j = t * kAttnTK + lane;
-        const bool ok = j < a.K && raw >= 0 && raw < a.N;
+        const bool ok = j < klen && raw >= 0 && raw < a.N;
         bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
         rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
       }
@@ -481,7 +491,8 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
   const int b = static_cast<int>(grow / a.S);
   const int s = static_cast<int>(grow % a.S);
   const int hbase = hg * 64;
-  const int ntiles = a.ntiles;
+  const int klen = bwd_row_len(a, b, s);
+  const int ntiles = a.ntiles > 0 ? (klen + kAttnTK - 1) / kAttnTK : 0;  // tiles of this row
   constexpr int CPR = D / 8;
 
   // Q and dO of the row's 64 heads into LDS (zero past H).  Every load of a
@@ -511,7 +522,7 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
       *reinterpret_cast<u32x4*>(qd_lds + m * DS::QD + h * DS::QROW + c * 16) = v[i];
     }
   }
-  const uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * ntiles * kCoefTile;
+  const uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * a.ntiles * kCoefTile;
   // each thread moves 2 x 16 bytes of a tile's coefficient block
   u32x4 cnext[2];
   auto coef_load = [&](int t) {
@@ -542,7 +553,7 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
   const int bh = 8 * g + (i16 >> 2);
   const uint32_t cf0 = lds_addr(coef_lds) + ((bh >> 4) * 64 + (i16 & 3) * 16 + (bh & 15)) * 16;
 
-  const int64_t prow_base = (static_cast<int64_t>(lrow) * a.HG + hg) * (static_cast<int64_t>(ntiles) * kAttnTK);
+  const int64_t prow_base = (static_cast<int64_t>(lrow) * a.HG + hg) * (static_cast<int64_t>(a.ntiles) * kAttnTK);
 
   for (int t = 0; t < ntiles; ++t) {
     if (t + 1 < ntiles) coef_load(t + 1);
@@ -702,7 +713,8 @@ __global__ __launch_bounds__(kReduceThreads) void sparse_attn_bwd_dkv_reduce_ker
 // a valid index t, the sentinel B N (sorted last, never reduced) otherwise.
 __global__ void sparse_attn_bwd_pairs_kernel(const void* idx, int idx64, int64_t isb, int64_t iss, int64_t isk,
                                              int S, int N, int K, int64_t row0, int64_t n, uint32_t sentinel,
-                                             uint32_t* keys, uint32_t* vals) {
+                                             const int32_t* row_len, int64_t rlsb, int64_t rlss, uint32_t* keys,
+                                             uint32_t* vals) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n) return;
   const int64_t lrow = p / K;
@@ -711,7 +723,8 @@ __global__ void sparse_attn_bwd_pairs_kernel(const void* idx, int idx64, int64_t
   const int64_t b = grow / S, s = grow % S;
   const int64_t off = b * isb + s * iss + j * isk;
   const int64_t raw = idx64 ? static_cast<const int64_t*>(idx)[off] : static_cast<int64_t>(static_cast<const int32_t*>(idx)[off]);
-  keys[p] = (raw >= 0 && raw < N) ? static_cast<uint32_t>(b * N + raw) : sentinel;
+  const bool in_row = !row_len || j < row_len[b * rlsb + s * rlss];
+  keys[p] = (in_row && raw >= 0 && raw < N) ? static_cast<uint32_t>(b * N + raw) : sentinel;
   vals[p] = static_cast<uint32_t>(p);
 }
 
@@ -875,7 +888,8 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     const int64_t npairs = nr * a.K;
     const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
     hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, a.idx, a.idx64, a.isb, a.iss,
-                       a.isk, a.S, a.N, a.K, row0, npairs, static_cast<uint32_t>(nkeys), kin, vin);
+                       a.isk, a.S, a.N, a.K, row0, npairs, static_cast<uint32_t>(nkeys), a.row_len, a.rlsb, a.rlss,
+                       kin, vin);
     if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
     size_t tmp_bytes = pl.tmp_bytes;
     const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,
@@ -1000,13 +1014,16 @@ extern "C" int64_t si_sparse_attn_bwd_workspace_bytes(int64_t B, int64_t S, int6
   return static_cast<int64_t>(p.total);
 }
 
-extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
-                                  const float* attn_sink, const void* topk_idxs, int idx_is_i64,
-                                  const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
-                                  const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
-                                  int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale,
-                                  void* dq, const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
-                                  float* dsink, void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides, const void* kv,
+                                         const int64_t* kv_strides, const float* attn_sink, const void* topk_idxs,
+                                         int idx_is_i64, const int64_t* idx_strides, const void* o,
+                                         const int64_t* o_strides, const float* lse, const int64_t* lse_strides,
+                                         const void* dout, const int64_t* do_strides, int64_t B, int64_t S, int64_t H,
+                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
+                                         const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
+                                         float* dsink, void* workspace, int64_t workspace_bytes,
+                                         const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
+  if (row_len && !row_len_strides) return set_error(SI_ERR_INVALID, "null row_len strides");
   if (!q_strides || !kv_strides || !idx_strides || !o_strides || !lse_strides || !do_strides || !dq_strides ||
       !dkv_strides)
     return set_error(SI_ERR_INVALID, "null stride argument");
@@ -1062,6 +1079,11 @@ extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const
   a.N = static_cast<int>(N_kv); a.K = static_cast<int>(K);
   a.HG = static_cast<int>((H + 63) / 64);
   a.ntiles = N_kv > 0 ? static_cast<int>((K + kAttnTK - 1) / kAttnTK) : 0;
+  a.row_len = row_len;
+  if (row_len) {
+    a.rlsb = row_len_strides[0];
+    a.rlss = row_len_strides[1];
+  }
   a.scale = softmax_scale;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.idx64 = idx_is_i64 ? 1 : 0;
@@ -1077,6 +1099,19 @@ extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const
     case 512: return launch_bwd<512>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
     default: return launch_bwd<576>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
   }
+}
+
+extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                                  const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                                  const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
+                                  const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
+                                  int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale,
+                                  void* dq, const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
+                                  float* dsink, void* workspace, int64_t workspace_bytes, void* stream) {
+  return si_sparse_attn_bwd_ragged(q, q_strides, kv, kv_strides, attn_sink, topk_idxs, idx_is_i64, idx_strides, o,
+                                   o_strides, lse, lse_strides, dout, do_strides, B, S, H, D, N_kv, K, softmax_scale,
+                                   dq, dq_strides, dkv, dkv_strides, dsink, workspace, workspace_bytes, nullptr,
+                                   nullptr, stream);
 }
 
 static int inv_check(int64_t B, int64_t S, int64_t K, int64_t N, int64_t k_max) {
@@ -1128,7 +1163,8 @@ extern "C" int si_build_inverted_topk(const void* topk_idxs, int idx_is_i64, con
     const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
     hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, topk_idxs, idx_is_i64 ? 1 : 0,
                        idx_strides[0], idx_strides[1], idx_strides[2], static_cast<int>(S), static_cast<int>(n_kv),
-                       static_cast<int>(K), int64_t{0}, npairs, static_cast<uint32_t>(nkeys), kin, vin);
+                       static_cast<int>(K), int64_t{0}, npairs, static_cast<uint32_t>(nkeys), nullptr, int64_t{0},
+                       int64_t{0}, kin, vin);
     if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
     size_t tmp_bytes = pl.tmp_bytes;
     const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,

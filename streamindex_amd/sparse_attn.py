@@ -128,6 +128,7 @@ def sparse_attn_bwd(
     *,
     block_h: Optional[int] = None,
     workspace_bytes: Optional[int] = None,
+    row_len: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Backward of :func:`sparse_attn_fwd` from its saved ``o`` and ``lse``.
 
@@ -135,6 +136,8 @@ def sparse_attn_bwd(
     ``attn_sink``.  ``workspace_bytes`` caps the scratch memory (default:
     ``BWD_WORKSPACE_CAP`` or a quarter of the free device memory, whichever is
     smaller); the query rows are processed in as few chunks as fit it.
+    ``row_len`` as in :func:`sparse_attn_fwd` (an extension): columns at or
+    past it are masked and their tiles skipped.
     """
     del block_h
     assert q.is_cuda and kv.is_cuda and do.is_cuda
@@ -160,6 +163,10 @@ def sparse_attn_bwd(
     if softmax_scale is None:
         softmax_scale = D ** -0.5
     K = topk_idxs.shape[-1]
+    if row_len is not None:
+        assert row_len.is_cuda and row_len.shape == (B, S), "row_len must be [B, S] on the GPU"
+        if row_len.dtype != torch.int32:
+            row_len = row_len.to(torch.int32)
     q, kv, o, do = (t if _aligned(t) else t.contiguous() for t in (q, kv, o, do))
     attn_sink = attn_sink.contiguous()
     dq = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
@@ -174,12 +181,13 @@ def sparse_attn_bwd(
         if need < 0:
             raise ValueError(L.si_last_error().decode("utf-8", "replace"))
         ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=q.device)
-        rc = L.si_sparse_attn_bwd(
+        rc = L.si_sparse_attn_bwd_ragged(
             q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
             topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
             o.data_ptr(), _lib.strides(o), lse.data_ptr(), _lib.strides(lse), do.data_ptr(), _lib.strides(do),
             B, S, H, D, N_kv, K, float(softmax_scale), dq.data_ptr(), _lib.strides(dq),
             dkv.data_ptr(), _lib.strides(dkv), dsink.data_ptr(), ws.data_ptr(), ws.numel(),
+            None if row_len is None else row_len.data_ptr(), None if row_len is None else _lib.strides(row_len),
             _lib.stream_ptr(q.device))
     _lib.check(rc)
     return dq, dkv, dsink
@@ -244,11 +252,8 @@ class _SparseAttnFunc(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, kv, attn_sink, topk_idxs, o, lse, row_len = ctx.saved_tensors
-        if row_len is not None:
-            # the forward treated columns past row_len as masked: so does the backward
-            col = torch.arange(topk_idxs.shape[-1], device=topk_idxs.device)
-            topk_idxs = topk_idxs.masked_fill(col >= row_len.unsqueeze(-1).long(), -1)
-        dq, dkv, dsink = sparse_attn_bwd(q, kv, attn_sink, topk_idxs, o, lse, do.contiguous(), ctx.softmax_scale)
+        dq, dkv, dsink = sparse_attn_bwd(q, kv, attn_sink, topk_idxs, o, lse, do.contiguous(), ctx.softmax_scale,
+                                         row_len=row_len)
         return dq, dkv, dsink, None, None, None
 
 

@@ -113,6 +113,33 @@ def test_bwd_matches_oracle(cuda_device, D, H, K, i64):
     _run_and_check(2, 40, H, D, 200, K, seed=300 + D + H, i64=i64, label=f"D{D}H{H}K{K}")
 
 
+@pytest.mark.parametrize("D,H,i64,ws", [(576, 64, False, None), (64, 80, True, 1 << 20)])
+def test_bwd_row_len(cuda_device, D, H, i64, ws):
+    # Per-row column counts (0, inside a tile, on a tile edge, past K, random):
+    # bit-identical to the backward over the tail-masked rows (whose dead
+    # tiles run but contribute nothing), and equal to the oracle over them;
+    # the second case also runs in several workspace chunks.
+    B, S, N, K = 2, 24, 150, 100
+    q, kv, sink, idx, do = _inputs(B, S, H, D, N, K, seed=900 + D, i64=i64)
+    g = torch.Generator().manual_seed(D + 1)
+    rl = torch.randint(0, K + 20, (B, S), generator=g, dtype=torch.int32)
+    rl[:, :6] = torch.tensor([0, 1, 31, 32, 33, K], dtype=torch.int32)
+    rl = rl.cuda()
+    scale = D ** -0.5
+    col = torch.arange(K, device="cuda")
+    masked = idx.masked_fill(col >= rl.unsqueeze(-1).long(), -1)
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, scale, row_len=rl)
+    dq, dkv, dsink = sparse_attn_bwd(q, kv, sink, idx, o, lse, do, scale, row_len=rl, workspace_bytes=ws)
+    dq2, dkv2, dsink2 = sparse_attn_bwd(q, kv, sink, masked, o, lse, do, scale, workspace_bytes=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2) and torch.equal(dsink, dsink2)
+    rdq, rdkv, rds = _oracle(q, kv, sink, masked, o, lse, do, scale)
+    for b in range(B):
+        _close(dq[b].float().cpu().numpy(), rdq[b], f"row_len dq[b={b}]")
+        _close(dkv[b].float().cpu().numpy(), rdkv[b], f"row_len dkv[b={b}]")
+    assert np.all(np.abs(dsink.cpu().numpy() - rds) <= _dsink_bound(o, do, sink, lse))
+
+
 def test_reference_shapes_through_autograd(cuda_device):
     # tests/test_triton_sparse_attn_bwd.py:78-97 (seed 200, every 4th masked) and
     # :166-188 (B=2, every 3rd masked), gradients through torch.autograd
