@@ -645,18 +645,31 @@ struct DkvReduceArgs {
   int first, last;        // first / last chunk of query rows
 };
 
-constexpr int kReduceThreads = 256;
+// Reduction workgroup per key: 256 threads, G = 256 / CPR groups of CPR
+// threads (one 16-byte chunk of a row each); each group keeps 8 rows in
+// flight, so a long segment (a key picked by many queries, such as a
+// compressed KV row, collects as many rows as the chunk has queries) streams
+// 8 G rows at a time.
+template <int D>
+struct ReduceShape {
+  static constexpr int CPR = D / 8;
+  static constexpr int G = 256 / CPR;
+  static constexpr int NT = 256;
+};
 
 template <int D>
-__global__ __launch_bounds__(kReduceThreads) void sparse_attn_bwd_dkv_reduce_kernel(DkvReduceArgs r) {
-  constexpr int CPR = D / 8;                  // 16-byte chunks per row
-  constexpr int G = kReduceThreads / CPR;     // pair groups
+__global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce_kernel(DkvReduceArgs r) {
+  constexpr int CPR = ReduceShape<D>::CPR;    // 16-byte chunks per row
+  constexpr int G = ReduceShape<D>::G;        // pair groups
   __shared__ float red[G * D];
-  const int kid = blockIdx.x;
+  // Keys in reverse: in [kv ; kv_compressed] layouts the compressed rows,
+  // each selected by many queries, are the last keys, and their long
+  // segments start first instead of forming the grid's tail.
+  const int kid = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
   const int grp = threadIdx.x / CPR;
   const int c = threadIdx.x % CPR;
   float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (grp < G) {
+  {
     const int lo = r.seg_lo[kid], hi = r.seg_hi[kid];
     auto add_row = [&](int p) {
       const uint32_t pid = r.pair[p];
@@ -672,15 +685,40 @@ __global__ __launch_bounds__(kReduceThreads) void sparse_attn_bwd_dkv_reduce_ker
       }
     };
     int p = lo + grp;
-    for (; p + 3 * G < hi; p += 4 * G) {
-      add_row(p);
-      add_row(p + G);
-      add_row(p + 2 * G);
-      add_row(p + 3 * G);
-    }
-    for (; p < hi; p += G) add_row(p);
+    if (grp < G) {
+      if (r.HG == 1) {
+        // one head group: 8 pair ids, then 8 independent row loads in flight
+        for (; p + 7 * G < hi; p += 8 * G) {
+          uint32_t pid[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[grp * D + c * 8 + e] = sum[e];
+          for (int u = 0; u < 8; ++u) pid[u] = r.pair[p + u * G];
+          u32x4 v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int64_t lrow = pid[u] / static_cast<uint32_t>(r.K);
+            const int64_t j = pid[u] % static_cast<uint32_t>(r.K);
+            v[u] = *reinterpret_cast<const u32x4*>(r.prow + (lrow * r.KP + j) * D + c * 8);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              sum[2 * e] += bf_lo(v[u][e]);
+              sum[2 * e + 1] += bf_hi(v[u][e]);
+            }
+        }
+      } else {
+        for (; p + 7 * G < hi; p += 8 * G) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) add_row(p + u * G);
+        }
+      }
+      for (; p < hi; p += G) add_row(p);
+    }
+    if (grp < G) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[grp * D + c * 8 + e] = sum[e];
+    }
   }
   __syncthreads();
   if (threadIdx.x < CPR) {
@@ -922,8 +960,8 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     r.N = a.N;
     r.first = row0 == 0;
     r.last = row0 + nr >= total_rows;
-    hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D>), dim3(static_cast<unsigned>(nkeys)), dim3(kReduceThreads),
-                       0, st, r);
+    hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D>), dim3(static_cast<unsigned>(nkeys)),
+                       dim3(ReduceShape<D>::NT), 0, st, r);
     if ((rc = check_launch("sparse_attn_bwd_dkv_reduce_kernel"))) return rc;
   }
   hipLaunchKernelGGL(sparse_attn_bwd_dsink_kernel, dim3(static_cast<unsigned>(a.H)), dim3(256), 0, st, a.dsink_rows,
