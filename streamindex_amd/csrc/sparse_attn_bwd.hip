@@ -523,21 +523,25 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
     }
   }
   const uint16_t* coef_row = a.coef + (static_cast<int64_t>(lrow) * a.HG + hg) * a.ntiles * kCoefTile;
-  // each thread moves 2 x 16 bytes of a tile's coefficient block
-  u32x4 cnext[2];
-  auto coef_load = [&](int t) {
+  // Each thread moves 2 x 16 bytes of a tile's coefficient block.  The blocks
+  // are fetched two tiles ahead into two alternating register sets, so the
+  // wait before a block's LDS store leaves the previous and the current
+  // tile's row stores (18 + 18 per thread) in flight.
+  u32x4 c0[2], c1[2];
+  auto coef_load = [&](int t, u32x4 (&dst)[2]) {
     const u32x4* src = reinterpret_cast<const u32x4*>(coef_row + static_cast<int64_t>(t) * kCoefTile);
-    cnext[0] = src[threadIdx.x];
-    cnext[1] = src[threadIdx.x + kRowsThreads];
+    dst[0] = src[threadIdx.x];
+    dst[1] = src[threadIdx.x + kRowsThreads];
   };
-  auto coef_store = [&]() {
-    reinterpret_cast<u32x4*>(coef_lds)[threadIdx.x] = cnext[0];
-    reinterpret_cast<u32x4*>(coef_lds)[threadIdx.x + kRowsThreads] = cnext[1];
+  auto coef_store = [&](const u32x4 (&v)[2]) {
+    reinterpret_cast<u32x4*>(coef_lds)[threadIdx.x] = v[0];
+    reinterpret_cast<u32x4*>(coef_lds)[threadIdx.x + kRowsThreads] = v[1];
   };
   if (ntiles > 0) {
-    coef_load(0);
-    coef_store();
+    coef_load(0, c0);
+    coef_store(c0);
   }
+  if (ntiles > 1) coef_load(1, c0);
   __syncthreads();
 
   // A-fragment source (Q or dO; 8 heads of one dimension per lane after two
@@ -555,8 +559,10 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
 
   const int64_t prow_base = (static_cast<int64_t>(lrow) * a.HG + hg) * (static_cast<int64_t>(a.ntiles) * kAttnTK);
 
-  for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) coef_load(t + 1);
+  // Tile t: fetch the block of tile t+2 into `ahead`, compute, then publish
+  // the block of tile t+1 held in `held`.
+  auto tile = [&](int t, u32x4 (&ahead)[2], const u32x4 (&held)[2]) {
+    if (t + 2 < ntiles) coef_load(t + 2, ahead);
     // k-steps 0, 1: dS of heads 0..31, 32..63 against Q; 2, 3: P against dO
     bf16x8 bfr[4][2];
     auto b_read = [&](auto KC, auto NC) {
@@ -625,8 +631,12 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
     // Barriers without a release fence: they order only LDS (the row stores
     // need no ordering), so the stores of this tile stay in flight.
     attn_tile_barrier();  // every wave is done with this tile's coefficients
-    if (t + 1 < ntiles) coef_store();
+    if (t + 1 < ntiles) coef_store(held);
     attn_tile_barrier();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(t, c1, c0);
+    if (t + 1 < ntiles) tile(t + 1, c0, c1);
   }
 }
 
