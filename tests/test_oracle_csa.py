@@ -160,3 +160,33 @@ def test_planted_index_mistakes_are_caught():
     kept = O.topk(sc2, O.legal_limits(rows, 10, 4), 4)[0]
     assert (kept[rows >= 3] >= 0).any()  # the raw top-k lists legal -inf keys ...
     assert (O.csa_scores_topk_rows(sc2, rows, 4, 4, 0, 0) == -1).all()  # ... the CSA rows never do
+
+
+@pytest.mark.parametrize("S,n_win,n_comp,m_prime", [(40, 5, 9, 4), (300, 16, 64, 4), (257, 8, 3, 128)])
+def test_hca_row_len_matches_rows(S, n_win, n_comp, m_prime):
+    # the column counts the HCA composition passes to attention: nothing
+    # valid lies at or past them, and the last column before them is used
+    from streamindex_amd.hca import hca_row_len
+
+    rows = O.hca_idx_rows(np.arange(S), n_win, n_comp, m_prime, S)
+    rl = hca_row_len(1, S, n_win, n_comp, m_prime, "cpu")[0].numpy()
+    col = np.arange(rows.shape[1])
+    assert np.all(rows[col[None, :] >= rl[:, None]] == -1)
+    used = rl > n_win
+    assert np.all(rows[np.arange(S)[used], rl[used] - 1] >= 0)
+
+
+@pytest.mark.parametrize("S,T,m,top_k,n_win", [(40, 12, 4, 6, 5), (200, 50, 4, 16, 8), (64, 20, 2, 40, 3)])
+def test_csa_row_len_matches_rows(S, T, m, top_k, n_win):
+    # the fused CSA rows hold min(top_k, T, (s+1)//m) picks: finite scores,
+    # so every legal key is pickable; columns past the count are -1
+    from streamindex_amd.csa import csa_row_len
+
+    rng = np.random.default_rng(S + T)
+    scores = rng.standard_normal((S, T)).astype(np.float32)
+    rows = O.csa_scores_topk_rows(scores, np.arange(S), m, top_k, n_win, S)
+    rl = csa_row_len(1, S, n_win, top_k, T, m, "cpu")[0].numpy()
+    col = np.arange(rows.shape[1])
+    assert np.all(rows[col[None, :] >= rl[:, None]] == -1)
+    inside = (col[None, :] < rl[:, None]) & (col[None, :] >= n_win)
+    assert np.all(rows[inside] >= S)
