@@ -280,7 +280,7 @@ def csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=8, seed=4):
 
 
 def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m=4, n_win=128, top_k=512,
-                quantized=False):
+                quantized=False, bwd=False):
     """flash_csa_forward at V4-Flash dims; returns timings, stage split, peak HBM and parity.  With
     ``quantized`` the indexer runs under the production dtypes (fp4 q, fp8 k, quantised inside the
     timed call); the recall is then that of the quantised selection against the bf16 oracle."""
@@ -322,6 +322,23 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
         res["recall_vs_bf16_oracle" if quantized else "parity"] = csa_recall(qi, ki, w, rows_gpu, n_win, top_k, m,
                                                                             parity_rows)
         res["attn_max_abs_err"] = csa_attn_check(q, kv, kvc, sink, rows_gpu)
+    if bwd:
+        # backward of the composition through autograd (the indexer's picks carry no gradient)
+        qg, kvg, kvcg, sg = (t.detach().requires_grad_() for t in (q, kv, kvc, sink))
+        og = flash_csa_forward(qg, kvg, kvcg, qi, ki, w, sg, n_win=n_win, top_k=top_k, m=m,
+                               quantized_indexer=quantized)
+        do = torch.randn_like(og)
+        og.backward(do, retain_graph=True)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            og.backward(do, retain_graph=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res["bwd_ms"] = e0.elapsed_time(e1) / steps
+        res["bwd_tflops"] = 10.0 * n_h * d * nvalid / (res["bwd_ms"] * 1e-3) / 1e12
+        del qg, kvg, kvcg, sg, og, do
     del q, kv, kvc, qi, ki, w, rows_gpu
     torch.cuda.empty_cache()
     return res
@@ -507,7 +524,7 @@ def main():
 
     if not args.no_e2e:
         print("[bench] end-to-end CSA forward S=64K", file=sys.stderr, flush=True)
-        extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256)
+        extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256, bwd=not args.no_attn_bwd)
         print("[bench] end-to-end CSA forward S=1M (config[4])", file=sys.stderr, flush=True)
         extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
         print("[bench] end-to-end CSA forward S=1M with the fp4/fp8 indexer", file=sys.stderr, flush=True)
