@@ -915,7 +915,9 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
   int32_t* seg_hi = reinterpret_cast<int32_t*>(ws + pl.seg_hi);
   const unsigned end_bit = bwd_end_bit(nkeys);
   int rc;
-  if (a.ntiles == 0 && nkeys > 0) {
+  // No (row, key) pair contributes when there are no key tiles or no query
+  // rows: dkv is all zeros and the chunk loop below never writes it.
+  if ((a.ntiles == 0 || total_rows == 0) && nkeys > 0) {
     const int64_t tot = nkeys * D;
     const int64_t blocks = (tot + 255) / 256 < 65536 ? (tot + 255) / 256 : 65536;
     hipLaunchKernelGGL(sparse_attn_bwd_zero_dkv_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, dkv,

@@ -30,6 +30,7 @@ MAX_TOPK = 2048
 
 def _check_common(q: torch.Tensor, k_idx: torch.Tensor, weights: torch.Tensor):
     assert q.is_cuda and k_idx.is_cuda and weights.is_cuda
+    assert k_idx.device == q.device and weights.device == q.device, "q, k_idx and weights must share a device"
     assert q.dim() == 4 and k_idx.dim() == 3 and weights.dim() == 3
     B, S, H_I, D_I = q.shape
     B2, T, D_I2 = k_idx.shape
@@ -95,6 +96,7 @@ def _topk_launch(q, k_idx, weights, top_k, causal_mask, causal_ratio):
         if causal_mask.dtype != torch.bool:
             causal_mask = causal_mask != 0
         assert causal_mask.is_cuda and causal_mask.device == q.device
+        assert causal_mask.shape == (B, S, T), f"causal_mask must be [B,S,T]={(B, S, T)}"
         mask_ptr, mask_strides = causal_mask.data_ptr(), _lib.strides(causal_mask)
     ratio = 0 if causal_ratio is None else int(causal_ratio)
     if causal_ratio is not None and ratio <= 0:
@@ -211,6 +213,8 @@ def indexer_topk_q(
     the dequantised inputs ``q = value · q_scale``, ``k = value · k_scale``.
     """
     assert q_fp4.is_cuda and k_fp8.is_cuda and weights.is_cuda
+    for name, t in (("q_scale", q_scale), ("k_fp8", k_fp8), ("k_scale", k_scale), ("weights", weights)):
+        assert t.is_cuda and t.device == q_fp4.device, f"{name} must be a CUDA tensor on {q_fp4.device}"
     assert q_fp4.dim() == 4 and k_fp8.dim() == 3 and weights.dim() == 3
     B, S, H_I, Dh = q_fp4.shape
     B2, T, D_I = k_fp8.shape
@@ -252,6 +256,11 @@ def indexer_topk_q(
     out_scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q_fp4.device)
     mask_ptr, mask_strides = None, None
     if causal_mask is not None:
+        # the checks chunked_indexer_topk applies (chunked_indexer.py:79-86): the
+        # kernel reads the mask through its strides, so its shape and device matter
+        assert causal_mask.is_cuda and causal_mask.device == q_fp4.device, "causal_mask must be on q's device"
+        assert causal_mask.shape == (B, S, T), f"causal_mask must be [B,S,T]={(B, S, T)}, got {tuple(causal_mask.shape)}"
+        assert causal_ratio is None, "specify either causal_mask or causal_ratio, not both"
         if causal_mask.dtype != torch.bool:
             causal_mask = causal_mask != 0
         mask_ptr, mask_strides = causal_mask.data_ptr(), _lib.strides(causal_mask)

@@ -32,6 +32,16 @@ SUPPORTED_D = (32, 64, 128, 256, 512, 576)
 MAX_HEADS = 128
 
 
+def _check_device(dev: torch.device, **tensors) -> None:
+    """Every tensor argument the kernels dereference must live on ``dev``
+    (the reference asserts ``is_cuda`` on its inputs; a host pointer handed to
+    a kernel would fault instead of raising)."""
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        assert t.is_cuda and t.device == dev, f"{name} must be a CUDA tensor on {dev}, got {t.device}"
+
+
 def sparse_attn_fwd(
     q: torch.Tensor,
     kv: torch.Tensor,
@@ -59,6 +69,7 @@ def sparse_attn_fwd(
     """
     del block_h, block_n
     assert q.is_cuda and kv.is_cuda
+    _check_device(q.device, kv=kv, attn_sink=attn_sink, topk_idxs=topk_idxs, row_len=row_len)
     assert q.dim() == 4 and kv.dim() == 3
     assert q.dtype in (torch.bfloat16, torch.float16), f"Q must be bf16 or fp16, got {q.dtype}"
     assert kv.dtype == q.dtype
@@ -141,6 +152,7 @@ def sparse_attn_bwd(
     """
     del block_h
     assert q.is_cuda and kv.is_cuda and do.is_cuda
+    _check_device(q.device, kv=kv, attn_sink=attn_sink, topk_idxs=topk_idxs, o=o, lse=lse, do=do, row_len=row_len)
     assert q.shape == do.shape, "do must match q shape"
     assert q.dtype == kv.dtype == do.dtype
     assert attn_sink.dtype == torch.float32
@@ -219,6 +231,7 @@ def build_inverted_topk(topk_idxs: torch.Tensor, n_kv: int, k_max: int, *, block
     """
     del block_k
     assert topk_idxs.is_cuda and topk_idxs.dim() == 3
+    assert int(n_kv) >= 0 and int(k_max) >= 0, "n_kv and k_max must be non-negative"
     B, S, K = topk_idxs.shape
     if topk_idxs.dtype not in (torch.int32, torch.int64):
         topk_idxs = topk_idxs.to(torch.int64)

@@ -97,16 +97,19 @@ def check_indexer(q, k, w, top_k, got_idx, got_val, *, causal_ratio=None, mask=N
     T = k.shape[1]
     rows = np.arange(S, dtype=np.int64) if rows is None else np.asarray(rows, dtype=np.int64)
     stats = []
-    gi = got_idx.cpu().numpy()
-    gv = got_val.cpu().numpy()
+    # only the checked rows leave the device (q is 16 GiB at S = 1M)
+    sel = torch.as_tensor(rows, device=q.device)
+    local = np.arange(len(rows), dtype=np.int64)
     for b in range(B):
-        qb = bf16_bits(q[b])
+        qb = bf16_bits(q[b].index_select(0, sel))
         kb = bf16_bits(k[b])
-        wb = w[b].float().cpu().numpy()
+        wb = w[b].index_select(0, sel).float().cpu().numpy()
         lim = O.legal_limits(rows, T, causal_ratio)
-        sc = O.indexer_scores(qb, kb, wb, rows, lim=lim)
+        sc = O.indexer_scores(qb, kb, wb, local, lim=lim)
         mrows = None
         if mask is not None:
-            mrows = mask[b].cpu().numpy().astype(np.uint8)[rows]
-        stats.append(check_rows(sc, lim, top_k, gi[b][rows], gv[b][rows], mrows, label=f"{label}[b={b}]"))
+            mrows = mask[b].index_select(0, sel.to(mask.device)).cpu().numpy().astype(np.uint8)
+        gi = got_idx[b].index_select(0, sel.to(got_idx.device)).cpu().numpy()
+        gv = got_val[b].index_select(0, sel.to(got_val.device)).cpu().numpy()
+        stats.append(check_rows(sc, lim, top_k, gi, gv, mrows, label=f"{label}[b={b}]"))
     return stats

@@ -1,4 +1,5 @@
-"""Full-size indexer parity: S=65,536 (T=16,384) and S=1,048,576 (T=262,144),
+"""Full-size indexer parity: S=65,536 (T=16,384; config[1]), S=262,144
+(T=65,536; config[2]) and S=1,048,576 (T=262,144; config[4]'s indexer stage),
 H_I=64, D_I=128, top_k=512, causal_ratio=4 — the V4-Flash shapes.
 
 The CPU oracle cannot materialise these problems, so parity is checked two ways:
@@ -54,21 +55,66 @@ def _properties(q, k, w, idx, sc, top_k, ratio, nprobe=4096, seed=0):
     assert bool((err <= 1e-4 * (ref.abs() + scale)).all()), f"recomputed score error {err.max().item():.3e}"
 
 
+def _say(msg):
+    print(f"[test] {msg}", flush=True)
+
+
 def test_c1_s64k_full_size():
+    """config[1]: every row through the property checks, 4,096 sampled rows
+    (BASELINE's parity sample) plus the edge rows through the oracle gate."""
     S, ratio, top_k = 65536, 4, 512
     q, k, w = synth.indexer_inputs(1, S, 64, 128, ratio=ratio, seed=2026, device="cuda")
+    _say("config[1] chunked_indexer_topk S=65536 T=16384 k=512 seed=2026")
     idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)
     torch.cuda.synchronize()
     _properties(q, k, w, idx, sc, top_k, ratio)
-    rows = np.sort(np.random.default_rng(1).choice(S, 768, replace=False))
+    rows = np.sort(np.random.default_rng(1).choice(S, 4096, replace=False))
     rows = np.concatenate([[0, 1, 2, 3, 2047, 2048, S - 1], rows])
     st = check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, rows=np.unique(rows), label="S=64K")
     assert st[0]["recall_mean"] >= 0.999
 
 
+def test_c2_s256k_chunk_pairs_and_topk_range():
+    """config[2] (S=262,144, T=65,536): the chunk pairs of the reference's sweep
+    give bit-identical outputs (the fused kernel's selection is exact for any
+    partition, so chunk_s / chunk_t cannot change it); every row through the
+    property checks and 256 sampled rows through the oracle gate at top_k=512;
+    the ends of the top_k sweep (64, and 2048, the widest selection buffer) on
+    64 sampled rows each."""
+    S, ratio, top_k = 262144, 4, 512
+    q, k, w = synth.indexer_inputs(1, S, 64, 128, ratio=ratio, seed=2026, device="cuda")
+    outs = []
+    for cs, ct in ((1024, 4096), (2048, 8192), (8192, 32768)):
+        _say(f"config[2] chunked_indexer_topk S=262144 chunk_s={cs} chunk_t={ct}")
+        outs.append(chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=cs, chunk_t=ct))
+    torch.cuda.synchronize()
+    idx, sc = outs[0]
+    for i, s in outs[1:]:
+        assert torch.equal(i, idx) and torch.equal(s, sc), "chunk sizes changed the output"
+    del outs
+    _properties(q, k, w, idx, sc, top_k, ratio)
+    rng = np.random.default_rng(3)
+    rows = np.unique(np.concatenate([[0, 3, 4, 4095, 65535, 131071, S - 1], rng.choice(S, 256, replace=False)]))
+    st = check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, rows=rows, label="S=256K")
+    assert st[0]["recall_mean"] >= 0.999
+    del idx, sc
+    for kk in (64, 2048):
+        _say(f"config[2] chunked_indexer_topk S=262144 top_k={kk}")
+        i2, s2 = chunked_indexer_topk(q, k, w, kk, causal_ratio=ratio)
+        torch.cuda.synchronize()
+        _properties(q, k, w, i2, s2, kk, ratio, nprobe=1024)
+        rows = np.unique(np.concatenate([[S - 1, 8191], rng.choice(S, 64, replace=False)]))
+        st = check_indexer(q, k, w, kk, i2, s2, causal_ratio=ratio, rows=rows, label=f"S=256K k={kk}")
+        assert st[0]["recall_mean"] >= 0.999
+        del i2, s2
+    del q, k, w
+    torch.cuda.empty_cache()
+
+
 def test_c4_s1m_indexer_stage():
     S, ratio, top_k = 1 << 20, 4, 512
     q, k, w = synth.indexer_inputs(1, S, 64, 128, ratio=ratio, seed=2026, device="cuda")
+    _say("config[4] indexer stage chunked_indexer_topk S=1048576 T=262144 k=512")
     idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio)
     torch.cuda.synchronize()
     _properties(q, k, w, idx, sc, top_k, ratio)
@@ -76,3 +122,5 @@ def test_c4_s1m_indexer_stage():
     rows = np.unique(np.concatenate([[3, 4095, S - 1], rows]))
     st = check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, rows=rows, label="S=1M")
     assert st[0]["recall_mean"] >= 0.999
+    del q, k, w, idx, sc
+    torch.cuda.empty_cache()

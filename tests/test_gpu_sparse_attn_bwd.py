@@ -210,6 +210,38 @@ def test_bwd_empty_cases(cuda_device):
     _run_and_check(1, 24, H, D, 64, 32, 6, masked_rows=True, label="half-masked")
 
 
+def test_bwd_no_query_rows_zeroes_dkv(cuda_device):
+    """S = 0 with keys and slots present: dkv must come back as zeros (the
+    reference's fp32 accumulator starts at zero), not as whatever the output
+    buffer held.  dkv is pre-filled with NaN and passed through the C ABI."""
+    from streamindex_amd import _lib as L
+
+    H, D, N, K = 16, 64, 32, 16
+    q = torch.empty((1, 0, H, D), dtype=torch.bfloat16, device="cuda")
+    kv = torch.randn((1, N, D), device="cuda").to(torch.bfloat16)
+    sink = torch.zeros(H, dtype=torch.float32, device="cuda")
+    idx = torch.empty((1, 0, K), dtype=torch.int32, device="cuda")
+    o, do, dq = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    lse = torch.empty((1, 0, H), dtype=torch.float32, device="cuda")
+    dkv = torch.full_like(kv, float("nan"))
+    dsink = torch.full_like(sink, float("nan"))
+    lib = L.load()
+    need = lib.si_sparse_attn_bwd_workspace_bytes(1, 0, H, D, N, K, 1 << 30)
+    ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device="cuda")
+    rc = lib.si_sparse_attn_bwd(
+        q.data_ptr(), L.strides(q), kv.data_ptr(), L.strides(kv), sink.data_ptr(), idx.data_ptr(), 0,
+        L.strides(idx), o.data_ptr(), L.strides(o), lse.data_ptr(), L.strides(lse), do.data_ptr(), L.strides(do),
+        1, 0, H, D, N, K, D ** -0.5, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
+        dsink.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_ptr(q.device))
+    L.check(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(dkv, torch.zeros_like(dkv))
+    assert torch.equal(dsink, torch.zeros_like(dsink))
+    # the Python wrapper returns the same
+    _, dkv2, ds2 = sparse_attn_bwd(q, kv, sink, idx, o, lse, do)
+    assert torch.equal(dkv2, torch.zeros_like(dkv2)) and torch.equal(ds2, torch.zeros_like(ds2))
+
+
 def test_bwd_v4_shape_sampled(cuda_device):
     """D = 576, H = 64, K = 512 causal indices over N = S/4 keys: dq on
     sampled rows, dkv on sampled keys (every selecting row), dsink in full."""

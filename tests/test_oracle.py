@@ -389,3 +389,48 @@ def test_planted_mistakes_are_caught():
     p_wrong = np.exp(s) / np.exp(s).sum(-1, keepdims=True)  # sink dropped entirely
     assert not np.allclose(np.einsum("nhm,md->nhd", p_wrong, kv2), o, atol=1e-6)
 
+
+
+# ---------------------------------------------------------------------------
+# the CPU baseline (the reference's fp32 materialise path, op for op)
+# ---------------------------------------------------------------------------
+def _torch_inputs(rng, S, H, D, T):
+    qb, kb = _rand_bf16(rng, (S, H, D), D ** -0.5), _rand_bf16(rng, (T, D), D ** -0.5)
+    w = rng.standard_normal((S, H)).astype(np.float32)
+    q = torch.from_numpy(qb.view(np.int16)).view(torch.bfloat16).unsqueeze(0)
+    k = torch.from_numpy(kb.view(np.int16)).view(torch.bfloat16).unsqueeze(0)
+    return qb, kb, w, q, k, torch.from_numpy(w).unsqueeze(0)
+
+
+@pytest.mark.parametrize("S,T,k", [(128, 32, 10), (96, 24, 40), (4096 // 16, 1024 // 16, 512 // 16)])
+def test_torch_materialize_baseline_matches_c_oracle(S, T, k):
+    from oracle.torch_materialize import materialize_topk
+
+    rng = np.random.default_rng(S + T + k)
+    H, D, ratio = 16, 32, 4
+    qb, kb, w, q, kk, wt = _torch_inputs(rng, S, H, D, T)
+    t_idx, t_val = materialize_topk(q, kk, wt, k, ratio)
+    assert t_idx.shape == (1, S, min(k, T)) and t_idx.dtype == torch.int64 and t_val.dtype == torch.float32
+    ref_idx, ref_val, _ = O.indexer_topk_rows(qb, kb, w, min(k, T), causal_ratio=ratio)
+    got = t_idx[0].numpy()
+    # fp32 scores of distinct Gaussian keys: same sets and order as the fp64 oracle
+    assert O.set_overlap_recall(ref_idx, got).min() == 1.0
+    fin = np.isfinite(ref_val)
+    assert np.array_equal(got >= 0, fin)
+    assert np.allclose(t_val[0].numpy()[fin], ref_val[fin], rtol=1e-5, atol=1e-6)
+    # rows s < ratio - 1 have no legal key: every slot is -1 after the post-mask
+    assert np.all(got[: ratio - 1] == -1)
+
+
+def test_torch_materialize_post_mask_is_needed():
+    """Without the post-mask the -inf slots of short rows carry arbitrary
+    indices, which the recall metric would count as wrong picks."""
+    from oracle.torch_materialize import materialize_topk
+
+    rng = np.random.default_rng(5)
+    S, H, D, T, k, ratio = 64, 16, 32, 16, 8, 4
+    qb, kb, w, q, kk, wt = _torch_inputs(rng, S, H, D, T)
+    idx, val = materialize_topk(q, kk, wt, k, ratio)
+    short = torch.isinf(val[0])
+    assert bool(short.any()) and bool((idx[0][short] == -1).all())
+    assert bool((idx[0][~short] >= 0).all())
