@@ -199,6 +199,30 @@ int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides, const voi
                               const int64_t* row_len_strides, void* stream);
 
 /*
+ * si_sparse_attn_bwd_ragged without allocation: the workspace is a
+ * file-scope device array of si_sparse_attn_bwd_noalloc_scratch_bytes()
+ * bytes (128 MiB) that each GPU holds from library load until the process
+ * ends; nothing is allocated and no workspace argument is taken.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (HIP graph capture, tight training loops, harnesses that forbid
+ * hipMalloc).  Arguments and results as si_sparse_attn_bwd_ragged.  Rows are
+ * processed in chunks that fit the scratch; a problem whose smallest plan
+ * (one query row per chunk: 4*B*S*64*ceil(H/64) + 8*B*N_kv + 4*B*N_kv*D bytes
+ * plus one row's coefficients, per-slot rows and sort buffers) exceeds it is
+ * rejected with SI_ERR_UNSUPPORTED before any launch.  All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU (other threads or
+ * streams) race.
+ */
+int64_t si_sparse_attn_bwd_noalloc_scratch_bytes(void);
+int si_sparse_attn_bwd_noalloc(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                               const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                               const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
+                               const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
+                               int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
+                               const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides, float* dsink,
+                               const int32_t* row_len, const int64_t* row_len_strides, void* stream);
+
+/*
  * Inverted top-k index.  Replaces flash_sparse/triton/inverted_topk.py:75-128
  * (build_inverted_topk).
  *   topk_idxs [B,S,K] int32 / int64 (strides in elements); keys outside [0, n_kv) ignored.
