@@ -1,7 +1,7 @@
 """Benchmark of the StreamIndex MI355X hot path.
 
 Metric: V4-Flash indexer ms at S=64K and S=1M, MFMA utilisation, peak HBM.
-Default workload: the V4-Flash indexer on one MI355X,
+Default workload (config[1]): the V4-Flash indexer on one MI355X,
 B=1, S=65,536, H_I=64, D_I=128, T=16,384, top_k=512, causal_ratio=4,
 chunk_s=2048, chunk_t=8192, seeded bf16/fp32 synthetic inputs resident in HBM.
 One "step" = one ``chunked_indexer_topk`` call (one launch of the fused
@@ -11,22 +11,25 @@ Printed (one JSON line, rank 0):
   value          ms per call at S=64K (lower is better)
   roofline       MFMA bound of the dominant kernel: algorithmic FLOPs
                  (2·H_I·D_I per causally legal (s,t) pair) / mean kernel time
-                 from HIP events on the launch stream, vs 2516.6 TFLOP/s
+                 from HIP events on the launch stream, vs 2516.6 TFLOP/s;
+                 traffic = HBM bytes per launch from this run's FETCH_SIZE /
+                 WRITE_SIZE counters (scaled by a plain copy's readings)
+  counters       rocprofv3 passes run by this bench in a child process on the
+                 same GPU: MFMA-busy fraction and shader clock of the indexer
+                 at config[1], HBM bytes of the indexer and of config[3]
   peak_hbm_gib   max_memory_allocated delta during one call (inputs excluded)
-  parity         recall vs the CPU oracle on sampled rows
-  cpu_baseline   the CPU oracle on a bounded row sample, extrapolated
-  extra          S=1M indexer time (config[4] indexer stage), the indexer over
-                 the production V4 dtypes (fp4 q, fp8 k) at S=64K and 1M vs the
-                 fp8 MFMA peak with sampled-row recall, sparse-attn fwd
-                 at config[3] with its HBM roofline, the sparse-attn backward
-                 at config[3] (dq, dkv, dsink from the saved o / lse; sampled
-                 dq rows and dkv keys against the oracle), and the end-to-end CSA
-                 forward (flash_csa_forward: fused indexer -> int32 window +
-                 compressed index rows -> sparse attention, 64 heads, d=576,
-                 n_win=128) at S=64K and at S=1M (config[4]) with its stage
-                 split, peak HBM and sampled-row recall against the oracle,
-                 and at S=1M again with the fp4/fp8 indexer (the production
-                 V4 indexer dtypes, quantised inside the timed call)
+  parity         config[1] against the CPU oracle on 4,096 sampled rows:
+                 recall, exact sets where the k-th gap is wide, score error
+  cpu_baseline   the reference's CPU path (fp32 torch materialise -> mask ->
+                 topk -> post-mask, oracle/torch_materialize.py) run in full
+                 at config[0] on this host, 1 warm-up + 3 timed, scaled to
+                 the config[1] job by dense (s,t) pairs
+  extra          config[0] on the GPU; config[2] (S=262,144) with its chunk
+                 pairs and top_k sweep; S=1M (config[4] indexer stage) at
+                 top_k 512 and 1024; the fp4/fp8 indexer; sparse attention at
+                 config[3] on config[1]'s own indexer output with sampled
+                 parity (and on random indices); its backward; the end-to-end
+                 CSA forward at S=64K and S=1M (config[4]); the HCA forward
 """
 
 from __future__ import annotations
@@ -54,10 +57,14 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5033.2   # MI355X dense fp8 MFMA (the fp4 x fp8 product runs at the fp8 rate)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # Reference timings on one H200 (other hardware; context only):
-# benchmarks/results/2026-04-27/scaling_v4_flash_indexer_final.log:10,14
-REF_H200_MS = {65536: 122.2, 1048576: 30899.6}
+# benchmarks/results/2026-04-27/scaling_v4_flash_indexer_final.log:10,12,14
+REF_H200_MS = {65536: 122.2, 262144: 1935.3, 1048576: 30899.6}
+REF_H200_GIB = {65536: 0.59, 262144: 1.71, 1048576: 6.21}
+# top_k sweep at S=262,144: benchmarks/results/2026-05-01/RESULTS.md:35-42
+REF_H200_TOPK_S256K_MS = {64: 1754, 256: 1881, 512: 1934, 1024: 1996, 2048: 2217}
+# V4-Pro point, top_k=1024 at S=1M: RESULTS.md:86-96 (ms, GiB)
+REF_H200_S1M_K1024 = (31973.3, 12.27)
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def _events_time(fn, iters: int, stream: torch.cuda.Stream) -> float:
@@ -89,34 +96,82 @@ def _bits(t: torch.Tensor) -> np.ndarray:
 
 
 def indexer_parity_and_cpu(q, k, w, idx, sc, ratio, top_k, nrows, seed=0):
-    """Oracle on `nrows` sampled rows: recall + CPU time (the cpu_baseline leg)."""
+    """config[1] against the CPU oracle on `nrows` sampled rows: recall, the
+    exact-set gate where the oracle's k-th gap is wide (1e-4 of the row scale),
+    the score error at every returned index, and the C oracle's own time on
+    those rows (a secondary, labelled CPU figure)."""
     from oracle import oracle as O
 
     S = q.shape[1]
     T = k.shape[1]
     rng = np.random.default_rng(seed)
     rows = np.sort(rng.choice(S, size=min(nrows, S), replace=False)).astype(np.int64)
-    qb = _bits(q[0, torch.from_numpy(rows).to(q.device)])
+    sel = torch.from_numpy(rows).to(q.device)
+    qb = _bits(q[0, sel])
     kb = _bits(k[0])
-    wb = w[0, torch.from_numpy(rows).to(q.device)].float().cpu().numpy()
+    wb = w[0, sel].float().cpu().numpy()
     local = np.arange(len(rows), dtype=np.int64)
     O.lib()
     t0 = time.perf_counter()
     lim = O.legal_limits(rows, T, ratio)
     scores = O.indexer_scores(qb, kb, wb, local, lim=lim)  # rows' own q/w are packed densely
-    ref_idx, _ = O.topk(scores, lim, top_k)
+    ref_idx, ref_val = O.topk(scores, lim, top_k)
     cpu_s = time.perf_counter() - t0
-    got = idx[0].cpu().numpy()[rows]
+    got = idx[0, sel].cpu().numpy()
+    got_v = sc[0, sel].cpu().numpy().astype(np.float64)
     rec = O.set_overlap_recall(ref_idx, got)
-    pairs_sample = float(np.minimum(lim, T).sum())
+    # score of every returned (row, index) against the oracle's fp64 score there
+    valid = got >= 0
+    rr, cc = np.nonzero(valid)
+    ref_at = scores[rr, got[rr, cc]]
+    row_scale = np.array([np.abs(scores[r, :max(1, int(lim[r]))]).mean() if lim[r] > 0 else 1.0
+                          for r in range(len(rows))])
+    rel = np.abs(got_v[rr, cc] - ref_at) / (np.abs(ref_at) + row_scale[rr])
+    # exact index set wherever the k-th / (k+1)-th gap exceeds 1e-4 of the row scale
+    wide = np.zeros(len(rows), dtype=bool)
+    for r in range(len(rows)):
+        n_leg = int(lim[r])
+        if n_leg <= top_k:
+            wide[r] = True  # every legal key is selected: the set is forced
+            continue
+        kth = ref_val[r, top_k - 1]
+        legal = scores[r, :n_leg]
+        below = legal[legal < kth]
+        nxt = below.max() if below.size else -np.inf
+        wide[r] = np.sum(legal >= kth) == top_k and (kth - nxt) > 1e-4 * row_scale[r]
     return {
         "rows": int(len(rows)),
         "recall_mean": float(rec.mean()),
         "recall_min": float(rec.min()),
         "exact_rows_frac": float((rec == 1.0).mean()),
+        "wide_gap_rows": int(wide.sum()),
+        "wide_gap_rows_exact": int((rec[wide] == 1.0).sum()),
+        "max_score_rel_err": float(rel.max()) if rel.size else 0.0,
         "cpu_s": cpu_s,
-        "pairs_sample": pairs_sample,
+        "pairs_sample": float(np.minimum(lim, T).sum()),
     }
+
+
+def cpu_baseline_c0(ratio, top_k):
+    """The reference's CPU path (oracle/torch_materialize.py: fp32 einsum ->
+    ReLU -> weighted head sum -> mask -> topk -> post-mask) run in full at
+    config[0] on this host: 1 warm-up + 3 timed runs."""
+    from oracle.torch_materialize import time_materialize
+
+    q, k, w = synth.indexer_inputs(1, 4096, 64, 128, ratio=ratio, seed=2026, device="cpu")
+    res = time_materialize(q, k, w, top_k, ratio, warmup=1, repeats=3)
+    res.pop("out")
+    return res
+
+
+def run_c0_gpu(ratio, top_k, steps):
+    """config[0] (S=4,096) on the GPU, for the same-workload comparison with the CPU baseline."""
+    dev = torch.device("cuda:0")
+    q, k, w = synth.indexer_inputs(1, 4096, 64, 128, ratio=ratio, seed=2026, device=dev)
+    fn = lambda: chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    return _events_time(fn, steps, torch.cuda.current_stream(dev))
 
 
 def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, seed=2026):
@@ -137,6 +192,180 @@ def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, s
     idx, sc = fn()
     torch.cuda.synchronize()
     return dict(q=q, k=k, w=w, T=T, ms=ms, wall_ms=wall, peak_gib=peak, flops=flops, idx=idx, sc=sc)
+
+
+def run_indexer_sweep(q, k, w, ratio, top_ks, steps):
+    """chunked_indexer_topk at each top_k on the same resident inputs: ms
+    (HIP events), TFLOP/s and peak HBM (outputs; the kernel needs no workspace)."""
+    dev = q.device
+    S, T, H, D = q.shape[1], k.shape[1], q.shape[2], q.shape[3]
+    flops = synth.indexer_flops(S, T, H, D, ratio)
+    out = {}
+    for kk in top_ks:
+        fn = lambda: chunked_indexer_topk(q, k, w, kk, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)  # noqa: E731
+        fn()
+        torch.cuda.synchronize()
+        peak = _peak_gib(fn)
+        ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
+        out[str(kk)] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                        "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "peak_hbm_gib": peak}
+    return out
+
+
+def run_c2(ratio, steps):
+    """config[2]: S=262,144, T=65,536 — time, TFLOP/s and peak HBM at top_k=512;
+    the reference's chunk pairs give bit-identical outputs; the top_k sweep of
+    benchmarks/results/2026-05-01/RESULTS.md:35-42 (H200 figures beside)."""
+    S = 262144
+    r = run_indexer(S, ratio, 512, 2048, 8192, steps, 1)
+    q, k, w = r["q"], r["k"], r["w"]
+    res = {"S": S, "T": r["T"], "ms": r["ms"], "tflops": r["flops"] / (r["ms"] * 1e-3) / 1e12,
+           "mfma_frac": r["flops"] / (r["ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "peak_hbm_gib": r["peak_gib"],
+           "reference_h200_ms": REF_H200_MS[S], "reference_h200_gib": REF_H200_GIB[S]}
+    same = True
+    for cs, ct in ((1024, 4096), (8192, 32768)):
+        i2, s2 = chunked_indexer_topk(q, k, w, 512, causal_ratio=ratio, chunk_s=cs, chunk_t=ct)
+        same = same and bool(torch.equal(i2, r["idx"])) and bool(torch.equal(s2, r["sc"]))
+        del i2, s2
+    res["chunk_pairs_identical"] = same
+    del r["idx"], r["sc"]
+    sweep = run_indexer_sweep(q, k, w, ratio, (64, 256, 512, 1024, 2048), max(2, steps))
+    for kk, v in sweep.items():
+        v["reference_h200_ms"] = REF_H200_TOPK_S256K_MS[int(kk)]
+    res["top_k_sweep"] = sweep
+    del q, k, w, r
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Hardware counters of this run (rocprofv3 in a child process, same GPU)
+# ---------------------------------------------------------------------------
+# One pass per counter group (rocprofv3 does not split counters over passes):
+# the MFMA pass stays within 8 SQ and 2 GRBM counters, FETCH_SIZE takes 3 of
+# the 4 TCC counters and WRITE_SIZE 2, so they run separately.
+COUNTER_PASSES = (
+    ("mfma", ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "GRBM_GUI_ACTIVE", "GRBM_COUNT")),
+    ("fetch", ("FETCH_SIZE",)),
+    ("write", ("WRITE_SIZE",)),
+)
+N_SIMD = 1024           # 256 CUs x 4 SIMDs
+N_XCD = 8               # GRBM_GUI_ACTIVE is summed over the XCDs
+MFMA_FLOP = 32 * 32 * 16 * 2   # v_mfma_f32_32x32x16_bf16
+COPY_MIB = 1024         # plain device copy used to scale the byte counters
+
+
+def counter_child(ratio=4, top_k=512):
+    """The workload the counter passes profile: config[1]'s indexer (1 warm-up
+    + 3 launches), sparse attention at config[3] on its output (1 + 2), and a
+    plain 1 GiB device copy (x3) that calibrates the byte counters."""
+    dev = torch.device("cuda:0")
+    q, k, w = synth.indexer_inputs(1, 65536, 64, 128, ratio=ratio, seed=2026, device=dev)
+    for _ in range(4):
+        idx, _ = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)
+    torch.cuda.synchronize()
+    del q, k, w
+    qa, kv, sink = synth.sparse_attn_inputs(1, 65536, 64, 576, 16384, seed=2027, device=dev)
+    for _ in range(3):
+        o, lse = sparse_attn_fwd(qa, kv, sink, idx, 576 ** -0.5)
+    torch.cuda.synchronize()
+    del qa, kv, o, lse, idx
+    n = COPY_MIB * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def _read_counters(path):
+    """rocprofv3 counter CSV -> {dispatch id: {"kernel", "ns", counter: value}}."""
+    import csv
+
+    out = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            d = out.setdefault(int(row["Dispatch_Id"]), {"kernel": row["Kernel_Name"],
+                                                         "ns": int(row["End_Timestamp"]) - int(row["Start_Timestamp"])})
+            d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    return out
+
+
+def _pick(disp, name, last):
+    rows = [v for _, v in sorted(disp.items()) if name in v["kernel"]]
+    return rows[-last:]
+
+
+def run_counters(timeout=240):
+    """Runs the counter passes over `counter_child` under rocprofv3 and returns
+    the indexer's MFMA-busy fraction, shader clock and counter-derived MFMA
+    utilisation, and the HBM bytes per launch of the indexer and of config[3]'s
+    attention (byte counters scaled by what they read for a plain copy)."""
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return {"error": "rocprofv3 not found"}
+    tmp = tempfile.mkdtemp(prefix="si_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    passes = {}
+    for name, ctrs in COUNTER_PASSES:
+        d = os.path.join(tmp, name)
+        cmd = [prof, "--pmc", *ctrs, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+               sys.executable, os.path.abspath(__file__), "--counter-child"]
+        print(f"[bench] counter pass {name}: {' '.join(ctrs)}", file=sys.stderr, flush=True)
+        p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                             start_new_session=True)
+        try:
+            log, _ = p.communicate(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            return {"error": f"counter pass {name} timed out after {timeout} s"}
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return {"error": f"counter pass {name}: no counter file (rc {p.returncode})",
+                    "log_tail": log.decode("utf-8", "replace")[-600:]}
+        passes[name] = _read_counters(files[0])
+    res = {"passes": [" ".join(c) for _, c in COUNTER_PASSES], "cmd": "rocprofv3 --pmc <pass> --output-format csv -- "
+           "python3 bench.py --counter-child"}
+    idx = _pick(passes["mfma"], "indexer_topk_kernel", 3)
+    if idx:
+        ns = float(np.mean([v["ns"] for v in idx]))
+        cyc = float(np.mean([v["GRBM_GUI_ACTIVE"] for v in idx])) / N_XCD
+        busy = float(np.mean([v["SQ_VALU_MFMA_BUSY_CYCLES"] for v in idx]))
+        insts = float(np.mean([v["SQ_INSTS_MFMA"] for v in idx]))
+        flops = synth.indexer_flops(65536, 16384, 64, 128, 4)
+        res["indexer_c1"] = {
+            "dispatches": len(idx), "avg_ms": ns * 1e-6,
+            "clock_ghz": cyc / ns,
+            "mfma_busy_pct": 100.0 * busy / N_SIMD / cyc,
+            "mfma_insts": insts,
+            "executed_mfma_flops": insts * MFMA_FLOP,
+            "algorithmic_flops": flops,
+            "mfma_util_pct_from_counters": 100.0 * insts * MFMA_FLOP / (ns * 1e-9) / 1e12 / PEAK_BF16_TFLOPS,
+            "valu_per_mfma": float(np.mean([v["SQ_INSTS_VALU"] for v in idx])) / max(insts, 1.0),
+        }
+    copies = _pick(passes["fetch"], "copyBuffer", 3)
+    wcopies = _pick(passes["write"], "copyBuffer", 3)
+    if copies and wcopies:
+        nbytes = COPY_MIB * (1 << 20)
+        fscale = nbytes / (float(np.mean([v["FETCH_SIZE"] for v in copies])) * 1024.0)
+        wscale = nbytes / (float(np.mean([v["WRITE_SIZE"] for v in wcopies])) * 1024.0)
+        res["fetch_scale"], res["write_scale"] = fscale, wscale
+        for key, kname, last in (("indexer_c1", "indexer_topk_kernel", 3), ("sparse_attn_c3", "sparse_attn_fwd_kernel", 2)):
+            f = _pick(passes["fetch"], kname, last)
+            wr = _pick(passes["write"], kname, last)
+            if f and wr:
+                fb = float(np.mean([v["FETCH_SIZE"] for v in f])) * 1024.0 * fscale
+                wb = float(np.mean([v["WRITE_SIZE"] for v in wr])) * 1024.0 * wscale
+                res.setdefault(key, {}).update({"hbm_read_bytes": fb, "hbm_write_bytes": wb,
+                                                "hbm_bytes_per_launch": fb + wb})
+    return res
 
 
 def run_indexer_q(S, ratio, top_k, steps, warmup, H=64, D=128, seed=2026, parity_rows=256):
@@ -176,11 +405,32 @@ def run_indexer_q(S, ratio, top_k, steps, warmup, H=64, D=128, seed=2026, parity
             "parity_rows": int(len(rows)), "recall_mean": float(rec.mean()), "recall_min": float(rec.min())}
 
 
-def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True):
-    """Forward (and optionally backward) sparse attention at one shape.  The
-    backward is timed from the forward's saved (o, lse) with dO ~ N(0,1)·0.5,
-    including its key sort and reduction; its FLOPs count the five products
-    per selected (row, key) pair (S and dP recomputed, dQ, dK, dV): 10 H D."""
+def attn_parity(q, kv, sink, idx, o, lse, nrows=64, seed=33):
+    """Sampled rows of a sparse-attention output against the oracle over the
+    same index rows: max |o - o_ref| (gate 2e-2) and max |lse - lse_ref|."""
+    from oracle import oracle as O
+
+    S, D = q.shape[1], q.shape[3]
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, 3, 4, S - 1], rng.choice(S, size=min(nrows, S), replace=False)]))
+    sel = torch.from_numpy(rows).to(q.device)
+    ir = idx[0, sel].long()
+    uniq = torch.unique(ir[ir >= 0])
+    remap = torch.where(ir >= 0, torch.searchsorted(uniq, ir.clamp(min=0)), torch.full_like(ir, -1))
+    ro, rl = O.sparse_attn_rows(_bits(q[0, sel]), _bits(kv[0, uniq]), sink.cpu().numpy(), remap.cpu().numpy(),
+                                D ** -0.5)
+    oe = float(np.abs(o[0, sel].float().cpu().numpy() - ro).max())
+    le = float(np.abs(lse[0, sel].cpu().numpy() - rl).max())
+    return {"rows": int(len(rows)), "o_max_abs_err": oe, "lse_max_abs_err": le, "pass": bool(oe <= 2e-2 and le <= 2e-3)}
+
+
+def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True, parity_rows=0):
+    """Forward (and optionally backward) sparse attention at one shape, on the
+    given indices (config[3]: config[1]'s indexer output) or on random distinct
+    causal ones.  The backward is timed from the forward's saved (o, lse) with
+    dO ~ N(0,1)·0.5, including its key sort and reduction; its FLOPs count the
+    five products per selected (row, key) pair (S and dP recomputed, dQ, dK,
+    dV): 10 H D."""
     dev = torch.device("cuda:0")
     q, kv, sink = synth.sparse_attn_inputs(1, S, H, D, T, seed=2027, device=dev)
     if idx is None:
@@ -196,6 +446,11 @@ def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=T
         res["ms"] = _events_time(fn, steps, stream)
         res["flops"] = 4.0 * H * D * nvalid
         res["unique_bytes"] = (q.numel() * 2 * 2 + idx.numel() * idx.element_size() + S * H * 4 + kv.numel() * 2)
+        if parity_rows:
+            o, lse = fn()
+            torch.cuda.synchronize()
+            res["parity"] = attn_parity(q, kv, sink, idx, o, lse, parity_rows)
+            del o, lse
     if bwd:
         o, lse = fn()
         g = torch.Generator(device=dev)
@@ -328,12 +583,16 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
         og = flash_csa_forward(qg, kvg, kvcg, qi, ki, w, sg, n_win=n_win, top_k=top_k, m=m,
                                quantized_indexer=quantized)
         do = torch.randn_like(og)
-        og.backward(do, retain_graph=True)
+        leaves = (qg, kvg, kvcg, sg)
+        # autograd.grad returns the gradients without accumulating into .grad
+        grads = torch.autograd.grad(og, leaves, do, retain_graph=True)
+        del grads
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(steps):
-            og.backward(do, retain_graph=True)
+            grads = torch.autograd.grad(og, leaves, do, retain_graph=True)
+            del grads
         e1.record(stream)
         torch.cuda.synchronize()
         res["bwd_ms"] = e0.elapsed_time(e1) / steps
@@ -386,12 +645,15 @@ def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=
         qg, kvg, kvcg, sg = (t.detach().requires_grad_() for t in (q, kv, kvc, sink))
         og = flash_hca_forward(qg, kvg, kvcg, sg, n_win=n_win, m_prime=m_prime)
         do = torch.randn_like(og)
-        og.backward(do, retain_graph=True)
+        leaves = (qg, kvg, kvcg, sg)
+        grads = torch.autograd.grad(og, leaves, do, retain_graph=True)
+        del grads
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(steps):
-            og.backward(do, retain_graph=True)
+            grads = torch.autograd.grad(og, leaves, do, retain_graph=True)
+            del grads
         e1.record(stream)
         torch.cuda.synchronize()
         res["bwd_ms"] = e0.elapsed_time(e1) / steps
@@ -413,10 +675,17 @@ def main():
     ap.add_argument("--chunk-s", type=int, default=2048)
     ap.add_argument("--chunk-t", type=int, default=8192)
     ap.add_argument("--parity-rows", type=int, default=4096)
-    ap.add_argument("--no-long", action="store_true", help="skip the S=1M indexer measurement")
+    ap.add_argument("--no-long", action="store_true", help="skip the S=1M indexer measurements")
+    ap.add_argument("--no-c2", action="store_true", help="skip the S=262,144 (config[2]) measurements")
     ap.add_argument("--no-attn", action="store_true", help="skip the sparse-attention measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (config[0] on the host)")
+    ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--counter-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
-    ap.add_argument("--only-attn", action="store_true", help="sparse-attention timing only (for profilers)")
+    ap.add_argument("--only-attn", action="store_true",
+                    help="config[3] sparse-attention timing only, on config[1]'s indexer output (for profilers)")
+    ap.add_argument("--only-attn-random", action="store_true",
+                    help="sparse-attention timing on random causal indices only (for profilers)")
     ap.add_argument("--only-attn-bwd", action="store_true", help="sparse-attention backward timing only (for profilers)")
     ap.add_argument("--only-indexer-q", type=int, default=0, metavar="S",
                     help="fp4/fp8 indexer timing only at sequence length S (for profilers)")
@@ -432,6 +701,9 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run 5 plain device copies of MIB MiB (scales HBM byte counters) and exit")
     args = ap.parse_args()
+    if args.counter_child:
+        counter_child(args.ratio, args.top_k)
+        return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -454,12 +726,21 @@ def main():
         print(json.dumps(rq), flush=True)
         return
     if args.only_attn_bwd:
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, bwd=True, fwd=False)
+        ri = run_indexer(65536, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
+        idx = ri["idx"]
+        del ri
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, idx=idx, bwd=True, fwd=False)
         print(json.dumps({"sparse_attn_bwd_ms": ra["bwd_ms"], "tflops": ra["bwd_flops"] / ra["bwd_ms"] / 1e9,
                           "parity": ra["bwd_parity"]}), flush=True)
         return
-    if args.only_attn:
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup)
+    if args.only_attn or args.only_attn_random:
+        idx = None
+        if args.only_attn:
+            ri = run_indexer(65536, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
+            idx = ri["idx"]
+            del ri
+            torch.cuda.empty_cache()
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, idx=idx)
         print(json.dumps({"sparse_attn_ms": ra["ms"], "tflops": ra["flops"] / ra["ms"] / 1e9,
                           "unique_gbps": ra["unique_bytes"] / ra["ms"] / 1e6}), flush=True)
         return
@@ -474,79 +755,126 @@ def main():
         sys.exit(1)
     _lib.load()
 
-    print(f"[bench] indexer S={args.seq} warmup={args.warmup} steps={args.steps}", file=sys.stderr, flush=True)
+    def say(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    say(f"indexer S={args.seq} warmup={args.warmup} steps={args.steps}")
     r = run_indexer(args.seq, args.ratio, args.top_k, args.chunk_s, args.chunk_t, args.steps, args.warmup)
     if args.only_indexer:
         print(json.dumps({"indexer_ms": r["ms"], "tflops": r["flops"] / r["ms"] / 1e9}), flush=True)
         return
     tflops = r["flops"] / (r["ms"] * 1e-3) / 1e12
-    print(f"[bench] indexer {r['ms']:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    say(f"indexer {r['ms']:.3f} ms, {tflops:.1f} TFLOP/s")
 
-    print(f"[bench] parity + cpu baseline on {args.parity_rows} sampled rows", file=sys.stderr, flush=True)
+    say(f"parity on {args.parity_rows} sampled rows")
     par = indexer_parity_and_cpu(r["q"], r["k"], r["w"], r["idx"], r["sc"], args.ratio, args.top_k,
                                  args.parity_rows)
     total_pairs = synth.legal_pairs(args.seq, r["T"], args.ratio)
-    cpu_ms_full = par["cpu_s"] * 1e3 * total_pairs / max(1.0, par["pairs_sample"])
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    del r["q"], r["k"], r["w"], r["idx"], r["sc"]
+    port_ms_full = par["cpu_s"] * 1e3 * total_pairs / max(1.0, par["pairs_sample"])
+    c1_idx = r["idx"]  # config[3]'s indices: config[1]'s own indexer output
+    del r["q"], r["k"], r["w"], r["sc"], r["idx"]
     torch.cuda.empty_cache()
 
-    extra = {"indexer_wall_ms_per_call": r["wall_ms"], "reference_h200_ms_s64k": REF_H200_MS[65536]}
+    extra = {"indexer_wall_ms_per_call": r["wall_ms"], "reference_h200_ms_s64k": REF_H200_MS[65536],
+             "reference_h200_gib_s64k": REF_H200_GIB[65536]}
+    extra["c0_gpu_ms"] = run_c0_gpu(args.ratio, args.top_k, max(5, args.steps))
+    cpu = None
+    if not args.no_cpu:
+        say("cpu baseline: the reference's fp32 materialise path at config[0] on the host")
+        cpu = cpu_baseline_c0(args.ratio, args.top_k)
+
+    if not args.no_attn:
+        say("sparse attention config[3] on config[1]'s indexer output")
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1, idx=c1_idx, bwd=not args.no_attn_bwd,
+                             parity_rows=64)
+        c3 = {"indices": "config[1] chunked_indexer_topk output (int64, -1 past the causal count)",
+              "ms": ra["ms"], "tflops": ra["flops"] / (ra["ms"] * 1e-3) / 1e12,
+              "mfma_frac": ra["flops"] / (ra["ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+              "unique_gbps": ra["unique_bytes"] / (ra["ms"] * 1e-3) / 1e9,
+              "valid_keys": ra["nvalid"], "parity": ra["parity"]}
+        c3["hbm_frac"] = c3["unique_gbps"] / PEAK_HBM_GBPS
+        if "bwd_ms" in ra:
+            c3["bwd"] = {"ms": ra["bwd_ms"], "tflops": ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12,
+                         "mfma_frac": ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         "peak_extra_gib": ra["bwd_peak_extra_gib"], "parity": ra["bwd_parity"]}
+        extra["sparse_attn_c3"] = c3
+        del ra
+        torch.cuda.empty_cache()
+        say("sparse attention on random causal indices (secondary)")
+        rr = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1)
+        extra["sparse_attn_random_idx"] = {"ms": rr["ms"], "tflops": rr["flops"] / (rr["ms"] * 1e-3) / 1e12,
+                                           "unique_gbps": rr["unique_bytes"] / (rr["ms"] * 1e-3) / 1e9}
+        del rr
+    del c1_idx
+    torch.cuda.empty_cache()
+
+    if not args.no_c2:
+        say("config[2]: indexer S=262144, chunk pairs, top_k sweep")
+        extra["c2_s256k"] = run_c2(args.ratio, 2)
+
     if not args.no_long:
-        print("[bench] indexer S=1M (config[4] indexer stage)", file=sys.stderr, flush=True)
+        say("indexer S=1M (config[4] indexer stage), top_k 512 and 1024")
         rl = run_indexer(1 << 20, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
         extra["s1m_ms"] = rl["ms"]
         extra["s1m_tflops"] = rl["flops"] / (rl["ms"] * 1e-3) / 1e12
+        extra["s1m_mfma_frac"] = extra["s1m_tflops"] / PEAK_BF16_TFLOPS
         extra["s1m_peak_hbm_gib"] = rl["peak_gib"]
         extra["reference_h200_ms_s1m"] = REF_H200_MS[1048576]
+        extra["reference_h200_gib_s1m"] = REF_H200_GIB[1048576]
+        k1024 = run_indexer_sweep(rl["q"], rl["k"], rl["w"], args.ratio, (1024,), 1)["1024"]
+        k1024["reference_h200_ms"], k1024["reference_h200_gib"] = REF_H200_S1M_K1024
+        extra["s1m_topk1024"] = k1024
         del rl
         torch.cuda.empty_cache()
     if not args.no_indexer_q:
-        print("[bench] fp4/fp8 indexer S=64K and S=1M", file=sys.stderr, flush=True)
+        say("fp4/fp8 indexer S=64K and S=1M")
         extra["indexer_q_s64k"] = run_indexer_q(65536, args.ratio, args.top_k, 5, 1)
         if not args.no_long:
             extra["indexer_q_s1m"] = run_indexer_q(1 << 20, args.ratio, args.top_k, 1, 1, parity_rows=64)
         torch.cuda.empty_cache()
-    if not args.no_attn:
-        print("[bench] sparse attention config[3]", file=sys.stderr, flush=True)
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1, bwd=not args.no_attn_bwd)
-        extra["sparse_attn_ms"] = ra["ms"]
-        if "bwd_ms" in ra:
-            extra["sparse_attn_bwd_ms"] = ra["bwd_ms"]
-            extra["sparse_attn_bwd_tflops"] = ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12
-            extra["sparse_attn_bwd_mfma_frac"] = extra["sparse_attn_bwd_tflops"] / PEAK_BF16_TFLOPS
-            extra["sparse_attn_bwd_peak_extra_gib"] = ra["bwd_peak_extra_gib"]
-            extra["sparse_attn_bwd_parity"] = ra["bwd_parity"]
-        extra["sparse_attn_tflops"] = ra["flops"] / (ra["ms"] * 1e-3) / 1e12
-        extra["sparse_attn_unique_gbps"] = ra["unique_bytes"] / (ra["ms"] * 1e-3) / 1e9
-        extra["sparse_attn_hbm_frac"] = extra["sparse_attn_unique_gbps"] / PEAK_HBM_GBPS
-        extra["sparse_attn_mfma_frac"] = extra["sparse_attn_tflops"] / PEAK_BF16_TFLOPS
 
     if not args.no_e2e:
-        print("[bench] end-to-end CSA forward S=64K", file=sys.stderr, flush=True)
+        say("end-to-end CSA forward S=64K")
         extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256, bwd=not args.no_attn_bwd)
-        print("[bench] end-to-end CSA forward S=1M (config[4])", file=sys.stderr, flush=True)
+        say("end-to-end CSA forward S=1M (config[4])")
         extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
-        print("[bench] end-to-end CSA forward S=1M with the fp4/fp8 indexer", file=sys.stderr, flush=True)
+        say("end-to-end CSA forward S=1M with the fp4/fp8 indexer")
         extra["csa_e2e_s1m_quantized_indexer"] = run_csa_e2e(1 << 20, 1, 1, 256, quantized=True)
-        print("[bench] end-to-end HCA forward S=64K", file=sys.stderr, flush=True)
+        say("end-to-end HCA forward S=64K")
         extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8, bwd=not args.no_attn_bwd)
+    torch.cuda.empty_cache()
 
+    counters = None
     traffic = None
-    tfile = {}
-    if os.path.exists(TRAFFIC_FILE):
-        try:
-            with open(TRAFFIC_FILE) as f:
-                tfile = json.load(f)
-            traffic = tfile.get("indexer_topk_c1_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
-    if "sparse_attn_ms" in extra and tfile.get("sparse_attn_c3_bytes_per_launch"):
-        # fabric bytes per launch (HBM byte counters: L2-missing gathers, q, o, indices) over the
-        # measured time: the bound of this kernel on random indices
-        fab = tfile["sparse_attn_c3_bytes_per_launch"] / (extra["sparse_attn_ms"] * 1e-3) / 1e9
-        extra["sparse_attn_fabric_gbps"] = fab
-        extra["sparse_attn_fabric_frac"] = fab / PEAK_HBM_GBPS
+    if not args.no_counters:
+        counters = run_counters()
+        ic = counters.get("indexer_c1", {}) if isinstance(counters, dict) else {}
+        traffic = ic.get("hbm_bytes_per_launch")
+        ac = counters.get("sparse_attn_c3", {}) if isinstance(counters, dict) else {}
+        if "sparse_attn_c3" in extra and ac.get("hbm_bytes_per_launch"):
+            fab = ac["hbm_bytes_per_launch"] / (extra["sparse_attn_c3"]["ms"] * 1e-3) / 1e9
+            extra["sparse_attn_c3"]["hbm_counter_gbps"] = fab
+            extra["sparse_attn_c3"]["hbm_counter_frac"] = fab / PEAK_HBM_GBPS
+            extra["sparse_attn_c3"]["hbm_bytes_per_launch"] = ac["hbm_bytes_per_launch"]
+
+    cpu_baseline = None
+    if cpu is not None:
+        dense_scale = (args.seq * (args.seq // args.ratio)) / (4096.0 * 1024.0)
+        cpu_baseline = {
+            "value": round(cpu["ms"] * dense_scale, 1),
+            "unit": f"ms (config[1] job, extrapolated x{dense_scale:.0f} by dense (s,t) pairs from the full "
+                    f"config[0] run)",
+            "cores": cpu["threads"], "kind": "port",
+            "sample": "config[0] in full (B=1, S=4096, T=1024, H_I=64, D_I=128, k=512, seed 2026): the reference's "
+                      "CPU path op for op in torch fp32 (einsum bshd,btd->bsht, relu, weighted head sum, -inf mask, "
+                      "topk, -1 post-mask; oracle/torch_materialize.py), 1 warm-up + 3 timed, median",
+            "config0_ms": round(cpu["ms"], 1), "config0_runs_ms": [round(x, 1) for x in cpu["runs_ms"]],
+            "config0_gpu_ms": round(extra["c0_gpu_ms"], 4),
+            "cpu_model": cpu["cpu_model"], "os_cpu_count": cpu["os_cpu_count"],
+            "port_sampled_c1": {"value_ms": round(port_ms_full, 1), "cpu_s": round(par["cpu_s"], 3),
+                                "note": f"C oracle (fp64, OpenMP) on the {par['rows']} parity rows of config[1], "
+                                        f"scaled by causally legal (s,t) pairs"},
+        }
 
     line = {
         "metric": "V4-Flash indexer ms @S=64K/1M, MFMA util %, peak HBM GB (1 GPU)",
@@ -569,12 +897,10 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "indexer_topk_kernel", "flops_per_launch": r["flops"]},
-        "parity": {k: par[k] for k in ("rows", "recall_mean", "recall_min", "exact_rows_frac")},
-        "cpu_baseline": {"value": round(cpu_ms_full, 1), "unit": "ms (extrapolated to the full S=64K job)",
-                         "cores": threads, "kind": "port",
-                         "sample": f"{par['rows']} sampled query rows of config[1] through the C oracle "
-                                   f"(scores in double + top-k), {par['cpu_s']:.2f} s measured, scaled by "
-                                   f"legal (s,t) pairs"},
+        "parity": {k: par[k] for k in ("rows", "recall_mean", "recall_min", "exact_rows_frac", "wide_gap_rows",
+                                       "wide_gap_rows_exact", "max_score_rel_err")},
+        "cpu_baseline": cpu_baseline,
+        "counters": counters,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
