@@ -35,8 +35,8 @@ struct IndexerArgs {
 };
 
 // Selection-buffer capacities the top-k kernel is instantiated for: 256,
-// 512, 1024, 2048 and 4096 keys per query row (capacity C serves
-// top_k <= C - 192).
+// 512, 1024, 1536, 2048 and 4096 keys per query row (capacity C serves
+// top_k <= C - 192; up to C = 1536 two workgroups share a CU).
 
 template <int HB, int D, int C>
 int launch_topk(const IndexerArgs& a, hipStream_t st);

@@ -14,6 +14,7 @@ static int dispatch_kcap(const IndexerArgs& a, hipStream_t st) {
   if (a.top_k <= 32) return launch_topk<HB, D, 256>(a, st);
   if (a.top_k <= 192) return launch_topk<HB, D, 512>(a, st);
   if (a.top_k <= 640) return launch_topk<HB, D, 1024>(a, st);
+  if (a.top_k <= 1152) return launch_topk<HB, D, 1536>(a, st);
   if (a.top_k <= 1536) return launch_topk<HB, D, 2048>(a, st);
   if (a.top_k <= 2048) return launch_topk<HB, D, 4096>(a, st);
   return set_error(SI_ERR_UNSUPPORTED, "top_k > 2048 is not supported");

@@ -241,15 +241,16 @@ __device__ __forceinline__ int legal_limit(const IndexerArgs& a, int s) {
 }
 
 // Launch shape of the top-k kernel per selection capacity C: four rows per
-// workgroup and 64-key tiles.  Up to C = 1024 a workgroup needs at most
-// 2*16 KiB (ring) + 4*8 KiB (selection) = 64 KiB of LDS and 256 VGPRs per
+// workgroup and 64-key tiles.  Up to C = 1536 a workgroup needs at most
+// 2*16 KiB (ring) + 4*12 KiB (selection) = 80 KiB of LDS and 256 VGPRs per
 // wave, so two workgroups share a CU; wider capacities run one per CU.
 template <int C>
 struct TopkShape {
   static constexpr int NW = 4;
   static constexpr int TILE_N = 64;
-  static constexpr int WAVES_PER_EU = C <= 1024 ? 2 : 1;
-  // K tiles in the LDS ring (a third buffer measured no faster at S = 64K).
+  static constexpr int WAVES_PER_EU = C <= 1536 ? 2 : 1;
+  // K tiles in the LDS ring: tile i+1 is copied while tile i is consumed (a
+  // third buffer measured no faster at S = 64K).
   static constexpr int RING = 2;
 };
 
@@ -282,7 +283,10 @@ void indexer_topk_kernel(IndexerArgs a) {
   // Compaction requests of the waves (double-buffered by tile parity) are
   // posted before each tile barrier, where LDS has room for them.
   constexpr int SEL_END = RING * TILE_BYTES + NW * C * 8;
-  constexpr bool SHARE_COMP = SEL_END + 2 * NW * 4 <= 160 * 1024;
+  // LDS per workgroup so that WAVES_PER_EU workgroups share a CU's 160 KiB.
+  constexpr int LDS_BUDGET = 160 * 1024 / TopkShape<C>::WAVES_PER_EU;
+  constexpr bool SHARE_COMP = SEL_END + 2 * NW * 4 <= LDS_BUDGET;
+  static_assert(SEL_END <= LDS_BUDGET, "ring + selection buffers exceed the LDS share");
   __shared__ __attribute__((aligned(16))) char lds[SEL_END + (SHARE_COMP ? 2 * NW * 4 : 0)];
   uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + RING * TILE_BYTES);
   int* const comp_req = reinterpret_cast<int*>(lds + SEL_END);
@@ -323,10 +327,7 @@ void indexer_topk_kernel(IndexerArgs a) {
   KTileLoader<D, TILE_N, NT> ld;
   ld.init(a.kst);
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
-  constexpr int LPT = KTileLoader<D, TILE_N, NT>::LPT;  // tile copies per thread
-#pragma unroll
-  for (int i = 0; i < RING - 1; ++i)
-    if (i < ntiles) ld.issue(kb, a.kst, i * TILE_N, a.T, lds + i * TILE_BYTES);
+  if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
 
   // Pipeline state carried across tiles.  Each of the G groups of a tile has
   // its own accumulator; the epilogue runs LAG = HB groups behind the MFMAs,
@@ -358,37 +359,46 @@ void indexer_topk_kernel(IndexerArgs a) {
     offer_tile(prev_p0, p1, prev_tbase, true, prev_mask);
   };
 
-  // Tile 0 landed (the copies of tiles 1..RING-2 may still be in flight).
-  if (RING == 3 && ntiles > 1) wait_vm_lgkm0<LPT>(); else wait_vm_lgkm0<0>();
+  // Tile 0 landed.
+  wait_vm_lgkm0<0>();
   __syncthreads();
 
-  int slot = 0;  // ring slot of tile `it`
-  for (int it = 0; it < ntiles; ++it) {
+  static_assert(RING == 2, "the tile loop is unrolled over the two ring slots");
+  // One tile; SLOT (the ring slot of tile `it`, it % 2) is a compile-time
+  // constant, so every LDS address of the tile is a per-lane base plus an
+  // immediate offset.
+  auto tile_step = [&](const int it, auto SLOTC) {
+    constexpr int slot = decltype(SLOTC)::value;
+    constexpr int fill = 1 - slot;
     const int tbase = it * TILE_N;
     if constexpr (MASKED) {  // issued before the tile copies so the waits below cover only the copies
       const int t = tbase + okey;
       cur_mask = t < my_lim ? mrow[static_cast<int64_t>(t) * a.mst] != 0 : false;
     }
-    // The slot of tile it+RING-1 last held tile it-1, which every wave
-    // finished before the barrier that ended the previous iteration.
-    const int fill = slot == 0 ? RING - 1 : slot - 1;
-    const bool more = it + RING - 1 < ntiles;
+    const bool more = it + 1 < ntiles;
+    const char* tile = lds + slot * TILE_BYTES;
+    int nblk = (my_lim - tbase + 31) / 32;
+    nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
+    // The B-fragment reads of a full tile's first block go out first: the
+    // compaction-request read and the next tile's copies overlap them, so the
+    // tile waits for one LDS round trip before its MFMAs.
+    bf16x8 kf[KS];
+    if (nblk == NB) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks]);
+    }
     int4 rq = int4{0, 0, 0, 0};
     if (SHARE_COMP && it > 0) rq = *reinterpret_cast<const int4*>(comp_req + ((it - 1) & 1) * NW);
-    if (more) ld.issue(kb, a.kst, (it + RING - 1) * TILE_N, a.T, lds + fill * TILE_BYTES);
+    // The slot of tile it+1 last held tile it-1, which every wave finished
+    // before the barrier that ended the previous tile.
+    if (more) ld.issue(kb, a.kst, (it + 1) * TILE_N, a.T, lds + fill * TILE_BYTES);
     // A compaction that some row asked for at the previous barrier runs now
     // in every row that is close to needing one, so that the workgroup waits
     // once for all of them instead of once per row.
     if (SHARE_COMP && (rq.x | rq.y | rq.z | rq.w) && sel.wants_compaction()) sel.compact(lane);
-    const char* tile = lds + slot * TILE_BYTES;
-    int nblk = (my_lim - tbase + 31) / 32;
-    nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
 
     if (nblk == NB) {
       // ---- full tile: software-pipelined groups ---------------------------
-      bf16x8 kf[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks]);
       __builtin_amdgcn_sched_barrier(0);  // all block-0 reads in flight before the first MFMA
       float p0 = 0.f, p1 = 0.f;
       auto phase = [&](auto PHC) {
@@ -397,6 +407,11 @@ void indexer_topk_kernel(IndexerArgs a) {
         constexpr bool last_use = (ph == HB - 1);     // block-0 fragments retire in this group
         constexpr int eg = (ph + G - LAG) % G;        // group whose epilogue runs now
         constexpr int emb = eg % HB;
+        // The wave's priority rises with its progress through the tile's MFMA
+        // groups: when both waves of a SIMD are in their MFMA sections, the
+        // one further along issues first, so the two drift apart instead of
+        // interleaving and reaching their loop tops together.
+        __builtin_amdgcn_s_setprio(ph);
         const float e = qfr.epilogue(acc[eg], emb);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -419,6 +434,7 @@ void indexer_topk_kernel(IndexerArgs a) {
         }
       };
       static_for<G>(phase);
+      __builtin_amdgcn_s_setprio(0);
       (void)p1;
       prev_p0 = p0;
       prev_tbase = tbase;
@@ -454,10 +470,17 @@ void indexer_topk_kernel(IndexerArgs a) {
     } else {
       if (sel.needs_compaction()) sel.compact(lane);
     }
-    // Tile it+1 must have landed; the copies of tile it+RING-1 may stay in flight.
-    if (RING == 3 && more) wait_vm_lgkm0<LPT>(); else wait_vm_lgkm0<0>();
+    // Tile it+1 must have landed.
+    wait_vm_lgkm0<0>();
     __syncthreads();
-    slot = slot == RING - 1 ? 0 : slot + 1;
+  };
+  {
+    int it = 0;
+    for (; it + 1 < ntiles; it += 2) {
+      tile_step(it, std::integral_constant<int, 0>{});
+      tile_step(it + 1, std::integral_constant<int, 1>{});
+    }
+    if (it < ntiles) tile_step(it, std::integral_constant<int, 0>{});
   }
 
   if (sel.needs_compaction()) sel.compact(lane);  // room for the pending offer
@@ -566,6 +589,7 @@ int launch_score(const IndexerArgs& a, hipStream_t st) {
   template int launch_topk<HB, D, 256>(const IndexerArgs&, hipStream_t);  \
   template int launch_topk<HB, D, 512>(const IndexerArgs&, hipStream_t);  \
   template int launch_topk<HB, D, 1024>(const IndexerArgs&, hipStream_t); \
+  template int launch_topk<HB, D, 1536>(const IndexerArgs&, hipStream_t); \
   template int launch_topk<HB, D, 2048>(const IndexerArgs&, hipStream_t); \
   template int launch_topk<HB, D, 4096>(const IndexerArgs&, hipStream_t);
 

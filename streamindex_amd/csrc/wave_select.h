@@ -126,8 +126,8 @@ template <int C>
 struct WaveSelect {
   static constexpr int E = C / kWave;   // 64-key rows in the buffer
   static constexpr int CMAX = C - 192;  // most keys a compaction keeps
-  static_assert(E >= 4 && (E & (E - 1)) == 0, "capacity must be 64 * 2^n, n >= 2");
-  // Capacities above 2048 serve only top_k <= C/2 (the full-width sort would not fit in registers).
+  static_assert(C % kWave == 0 && E >= 4 && E <= 64, "capacity must be 64 * E, 4 <= E <= 64");
+  // The final sort holds at most 32 keys per lane: capacities serve top_k <= 2048.
 
   uint64_t* buf;        // this wave's private LDS buffer, key at position p = buf[p]
   int n;                // keys held (wave-uniform)
@@ -269,35 +269,49 @@ struct WaveSelect {
   // Keeping close to top_k keys leaves the most room and the highest floor.
   __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, compact_cmax()); }
 
-  // Sorted top_k of the row, written through `out` (see TopkRowOut).
-  // When top_k fits in half the buffer, the held keys are first cut to at
-  // most C/2 (exactly top_k if more are held) so that only C/2 are sorted.
+  // Sorted top_k of the row, written through `out` (see TopkRowOut).  The
+  // held keys are cut to exactly top_k when more are held than the sort
+  // width, then the smallest power-of-two number of keys per lane that holds
+  // top_k (at most E) is bitonic-sorted in registers.
+  // Widest sort this capacity needs: keys per lane for the largest top_k it
+  // serves (C - 192), rounded up to a power of two.  It may exceed E (slots
+  // past the held count load as zero keys).
+  static constexpr int SE_CAP = (C - 192) <= 1 * kWave ? 1 : (C - 192) <= 2 * kWave ? 2
+                              : (C - 192) <= 4 * kWave ? 4 : (C - 192) <= 8 * kWave ? 8
+                              : (C - 192) <= 16 * kWave ? 16 : 32;
+
   __device__ __forceinline__ void finish(const TopkRowOut& out, int lane) {
-    constexpr int HE = E / 2;
-    if (top_k <= C / 2) {
-      if (n > C / 2) compact_to(lane, top_k, top_k);
-      wave_lds_sync();
-      uint64_t v[HE];
-#pragma unroll
-      for (int j = 0; j < HE; ++j) {
-        const int pos = j * kWave + lane;
-        v[j] = pos < n ? buf[pos] : 0ull;
-      }
-      wave_sort_desc<HE>(v, lane);
-      write_out<HE>(v, out, lane);
+    if (top_k <= 1 * kWave) {
+      finish_sorted<1>(out, lane);
+    } else if (top_k <= 2 * kWave) {
+      if constexpr (SE_CAP >= 2) finish_sorted<2>(out, lane);
+    } else if (top_k <= 4 * kWave) {
+      if constexpr (SE_CAP >= 4) finish_sorted<4>(out, lane);
+    } else if (top_k <= 8 * kWave) {
+      if constexpr (SE_CAP >= 8) finish_sorted<8>(out, lane);
+    } else if (top_k <= 16 * kWave) {
+      if constexpr (SE_CAP >= 16) finish_sorted<16>(out, lane);
     } else {
-      if constexpr (E <= 32) {
-        wave_lds_sync();
-        uint64_t v[E];
+      if constexpr (SE_CAP >= 32) finish_sorted<32>(out, lane);
+    }
+  }
+
+  template <int SE>
+  __device__ __forceinline__ void finish_sorted(const TopkRowOut& out, int lane) {
+    if (n > SE * kWave) compact_to(lane, top_k, top_k);
+    wave_lds_sync();
+    uint64_t v[SE];
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-          const int pos = j * kWave + lane;
-          v[j] = pos < n ? buf[pos] : 0ull;
-        }
-        wave_sort_desc<E>(v, lane);
-        write_out<E>(v, out, lane);
+    for (int j = 0; j < SE; ++j) {
+      const int pos = j * kWave + lane;
+      if (j < E) {
+        v[j] = pos < n ? buf[pos] : 0ull;
+      } else {
+        v[j] = 0ull;  // past the buffer (SE > E): never held
       }
     }
+    wave_sort_desc<SE>(v, lane);
+    write_out<SE>(v, out, lane);
   }
 
   // Keys of rank lane*EE+j are staged through LDS in rank order so that the
@@ -306,7 +320,12 @@ struct WaveSelect {
   __device__ __forceinline__ void write_out(const uint64_t (&v)[EE], const TopkRowOut& out, int lane) const {
     wave_lds_sync();
 #pragma unroll
-    for (int j = 0; j < EE; ++j) buf[lane * EE + j] = v[j];
+    for (int j = 0; j < EE; ++j) {
+      // Ranks past the buffer (EE * 64 > C) are never written out (top_k < C)
+      // and must not reach the next wave's buffer.
+      const int r = lane * EE + j;
+      if (EE * kWave <= C || r < C) buf[r] = v[j];
+    }
     wave_lds_sync();
     for (int e = lane; e < top_k; e += kWave) {
       const uint64_t k = buf[e];

@@ -75,7 +75,8 @@ def test_head_shapes(cuda_device, H, D):
     check_indexer(q, k, w, 40, idx, sc, label=f"H={H},D={D}")
 
 
-@pytest.mark.parametrize("top_k", [1, 7, 100, 128, 129, 700, 1024, 2048])
+@pytest.mark.parametrize("top_k", [1, 7, 64, 65, 100, 128, 129, 256, 257, 512, 513, 640, 641, 700, 1024, 1152,
+                                   1153, 1536, 1537, 2048])
 def test_topk_widths(cuda_device, top_k):
     q, k, w = _inputs(1, 96, 64, 128, 3000, 50 + top_k)
     idx, sc = chunked_indexer_topk(q, k, w, top_k)
@@ -104,6 +105,35 @@ def test_increasing_scores_worst_case(cuda_device):
     idx, sc = chunked_indexer_topk(q, k, w, 300)
     torch.cuda.synchronize()
     check_indexer(q, k, w, 300, idx, sc, label="rising")
+
+
+@pytest.mark.parametrize("top_k,T", [(1100, 6000), (700, 4096), (2000, 6000)])
+def test_increasing_scores_wide_selections(cuda_device, top_k, T):
+    # The rising-score worst case at the wide capacities (1536: two
+    # workgroups per CU, 4096): a compaction every few tiles.
+    B, S, H, D = 1, 12, 16, 32
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    q[..., 0] = 1.0
+    k = torch.zeros(B, T, D, dtype=torch.bfloat16)
+    k[0, :, 0] = torch.linspace(0.01, 8.0, T).to(torch.bfloat16)
+    w = torch.ones(B, S, H, dtype=torch.float32)
+    q, k, w = q.cuda(), k.cuda(), w.cuda()
+    idx, sc = chunked_indexer_topk(q, k, w, top_k)
+    torch.cuda.synchronize()
+    check_indexer(q, k, w, top_k, idx, sc, label=f"rising k={top_k}")
+
+
+def test_long_rows_v4_pro_topk(cuda_device):
+    # top_k = 1024 (the V4-Pro setting) over 20000 legal keys, then a bool mask at top_k = 1000
+    q, k, w = _inputs(1, 40, 64, 128, 20000, 62)
+    idx, sc = chunked_indexer_topk(q, k, w, 1024)
+    torch.cuda.synchronize()
+    check_indexer(q, k, w, 1024, idx, sc, label="long rows k=1024")
+    q, k, w = _inputs(1, 64, 64, 128, 4096, 63)
+    mask = torch.rand(1, 64, 4096, generator=torch.Generator().manual_seed(1)) < 0.7
+    idx, sc = chunked_indexer_topk(q, k, w, 1000, causal_mask=mask.cuda())
+    torch.cuda.synchronize()
+    check_indexer(q, k, w, 1000, idx, sc, mask=mask.cuda(), label="masked k=1000")
 
 
 def test_exact_ties_prefer_smaller_index(cuda_device):
