@@ -31,6 +31,10 @@ extern "C" {
 #define SI_ERR_UNSUPPORTED 2
 #define SI_ERR_LAUNCH 3
 
+/* Element type of the sparse-attention operands q, kv, o (and dO, dq, dkv). */
+#define SI_DTYPE_BF16 0
+#define SI_DTYPE_F16 1
+
 /* Version of this interface (incremented on any signature change). */
 int si_abi_version(void);
 
@@ -81,15 +85,17 @@ int si_indexer_score(const void* q, const int64_t* q_strides, const void* k_idx,
  * MQA sparse attention forward with attention sink.
  * Replaces flash_sparse/triton/sparse_attn_fwd.py:40-292 (_sparse_attn_fwd_kernel, sparse_attn_fwd).
  *
- *   q [B,S,H,D] bf16; kv [B,N_kv,D] bf16; attn_sink [H] fp32;
+ *   q [B,S,H,D] and kv [B,N_kv,D] of one element type, qkv_dtype SI_DTYPE_BF16 or
+ *   SI_DTYPE_F16 (sparse_attn_fwd.py:193,207 accept both); attn_sink [H] fp32;
  *   topk_idxs [B,S,K] int32 (idx_is_i64 = 0) or int64 (1); -1 or >= N_kv = masked.
- *   o [B,S,H,D] bf16 out; lse [B,S,H] fp32 out (natural log, sink included).
+ *   o [B,S,H,D] out, q's type; lse [B,S,H] fp32 out (natural log, sink included).
+ *   P is rounded to the element type before P.V, as the reference does.
  * Supported: H <= 128, D in {32,64,128,256,512,576}.
  */
 int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
                        const float* attn_sink, const void* topk_idxs, int idx_is_i64,
                        const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D, int64_t N_kv,
-                       int64_t K, float softmax_scale, void* o, const int64_t* o_strides, float* lse,
+                       int64_t K, float softmax_scale, int qkv_dtype, void* o, const int64_t* o_strides, float* lse,
                        const int64_t* lse_strides, void* stream);
 
 /*
@@ -103,7 +109,7 @@ int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, 
 int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
                               const float* attn_sink, const void* topk_idxs, int idx_is_i64,
                               const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D, int64_t N_kv,
-                              int64_t K, float softmax_scale, void* o, const int64_t* o_strides, float* lse,
+                              int64_t K, float softmax_scale, int qkv_dtype, void* o, const int64_t* o_strides, float* lse,
                               const int64_t* lse_strides, const int32_t* row_len, const int64_t* row_len_strides,
                               void* stream);
 
@@ -178,7 +184,7 @@ int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* kv, 
                        const float* attn_sink, const void* topk_idxs, int idx_is_i64, const int64_t* idx_strides,
                        const void* o, const int64_t* o_strides, const float* lse, const int64_t* lse_strides,
                        const void* dout, const int64_t* do_strides, int64_t B, int64_t S, int64_t H, int64_t D,
-                       int64_t N_kv, int64_t K, float softmax_scale, void* dq, const int64_t* dq_strides, void* dkv,
+                       int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype, void* dq, const int64_t* dq_strides, void* dkv,
                        const int64_t* dkv_strides, float* dsink, void* workspace, int64_t workspace_bytes,
                        void* stream);
 
@@ -193,7 +199,7 @@ int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides, const voi
                               const float* attn_sink, const void* topk_idxs, int idx_is_i64,
                               const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
                               const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
-                              int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
+                              int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype, void* dq,
                               const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides, float* dsink,
                               void* workspace, int64_t workspace_bytes, const int32_t* row_len,
                               const int64_t* row_len_strides, void* stream);
@@ -218,7 +224,7 @@ int si_sparse_attn_bwd_noalloc(const void* q, const int64_t* q_strides, const vo
                                const float* attn_sink, const void* topk_idxs, int idx_is_i64,
                                const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
                                const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
-                               int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
+                               int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype, void* dq,
                                const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides, float* dsink,
                                const int32_t* row_len, const int64_t* row_len_strides, void* stream);
 

@@ -78,6 +78,13 @@ def lib() -> ctypes.CDLL:
         L.oracle_sparse_attn.argtypes = [P, P, P, P, I, I, I, I, I, ctypes.c_double, P, P]
         L.oracle_sparse_attn_bwd.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, ctypes.c_double, P, I, P, P, P]
         L.oracle_sparse_attn.restype = None
+        L.oracle_sparse_attn_t.argtypes = [P, P, P, P, I, I, I, I, I, ctypes.c_double, ctypes.c_int, P, P]
+        L.oracle_sparse_attn_t.restype = None
+        L.oracle_sparse_attn_bwd_t.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, ctypes.c_double, P, I,
+                                               ctypes.c_int, P, P, P]
+        L.oracle_sparse_attn_bwd_t.restype = None
+        L.oracle_f16_to_f32.argtypes = [P, I, P]
+        L.oracle_f16_to_f32.restype = None
         _lib = L
     return _lib
 
@@ -175,10 +182,20 @@ def indexer_topk_rows(q_bits, k_bits, w, top_k: int, *, rows=None, causal_ratio=
 # ---------------------------------------------------------------------------
 # Sparse attention (C oracle)
 # ---------------------------------------------------------------------------
-def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float):
+def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bit patterns -> float32 through the C oracle's decoder."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32(_ptr(b), b.size, _ptr(out))
+    return out
+
+
+def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float,
+                     f16: bool = False):
     """Reference sparse attention for ``n`` rows of one batch.
 
-    q_bits [n,H,D] uint16, kv_bits [N,D] uint16, sink [H] f32, idx [n,K] int.
+    q_bits [n,H,D] uint16, kv_bits [N,D] uint16 (bf16 bits, or fp16 bits with
+    ``f16``), sink [H] f32, idx [n,K] int.
     Returns (o [n,H,D] float64, lse [n,H] float64).
     """
     n, H, D = q_bits.shape
@@ -190,16 +207,17 @@ def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, 
     idx = np.ascontiguousarray(idx, dtype=np.int64)
     o = np.empty((n, H, D), dtype=np.float64)
     lse = np.empty((n, H), dtype=np.float64)
-    lib().oracle_sparse_attn(_ptr(q_bits), _ptr(kv_bits), _ptr(sink), _ptr(idx), n, H, D, N, K, float(scale),
-                             _ptr(o), _ptr(lse))
+    lib().oracle_sparse_attn_t(_ptr(q_bits), _ptr(kv_bits), _ptr(sink), _ptr(idx), n, H, D, N, K, float(scale),
+                               1 if f16 else 0, _ptr(o), _ptr(lse))
     return o, lse
 
 
 def sparse_attn_bwd_rows(q_bits, kv_bits, o_bits, do_bits, sink, lse, idx, scale: float, *, want_dq: bool = True,
-                         keys: Optional[np.ndarray] = None, want_dkv: bool = True):
+                         keys: Optional[np.ndarray] = None, want_dkv: bool = True, f16: bool = False):
     """Reference sparse-attention backward for ``n`` rows of one batch.
 
-    q_bits, o_bits, do_bits [n,H,D] uint16; kv_bits [N,D] uint16; sink [H] f32;
+    q_bits, o_bits, do_bits [n,H,D] uint16; kv_bits [N,D] uint16 (bf16 bits,
+    or fp16 bits with ``f16``); sink [H] f32;
     lse [n,H] f32; idx [n,K] int.  Returns (dq [n,H,D] or None, dkv, dsink [H]),
     all float64.  dkv is [N,D] over every key, or [len(keys),D] for the listed
     keys only (the contributions of these ``n`` rows; a sampled check passes
@@ -222,10 +240,11 @@ def sparse_attn_bwd_rows(q_bits, kv_bits, o_bits, do_bits, sink, lse, idx, scale
         nslot = len(keys)
     dkv = np.zeros((nslot, D), dtype=np.float64) if want_dkv else None
     dsink = np.zeros(H, dtype=np.float64)
-    lib().oracle_sparse_attn_bwd(_ptr(arrs[0]), _ptr(arrs[1]), _ptr(arrs[2]), _ptr(arrs[3]), _ptr(sink), _ptr(lse),
-                                 _ptr(idx), n, H, D, N, K, float(scale),
-                                 None if key_slot is None else _ptr(key_slot), nslot if want_dkv else 0,
-                                 None if dq is None else _ptr(dq), None if dkv is None else _ptr(dkv), _ptr(dsink))
+    lib().oracle_sparse_attn_bwd_t(_ptr(arrs[0]), _ptr(arrs[1]), _ptr(arrs[2]), _ptr(arrs[3]), _ptr(sink), _ptr(lse),
+                                   _ptr(idx), n, H, D, N, K, float(scale),
+                                   None if key_slot is None else _ptr(key_slot), nslot if want_dkv else 0,
+                                   1 if f16 else 0, None if dq is None else _ptr(dq),
+                                   None if dkv is None else _ptr(dkv), _ptr(dsink))
     return dq, dkv, dsink
 
 

@@ -31,6 +31,34 @@ static inline float bf16_to_f32(uint16_t b) {
   return f;
 }
 
+/* IEEE binary16 bits to float (exact: every fp16 value is an fp32 value).
+ * Subnormals are man * 2^-24; exponent 31 is inf / NaN. */
+static inline float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t ex = (h >> 10) & 0x1Fu;
+  const uint32_t man = h & 0x3FFu;
+  uint32_t u;
+  if (ex == 0) {
+    const float mag = (float)man * 5.9604644775390625e-08f; /* 2^-24 */
+    memcpy(&u, &mag, sizeof u);
+    u |= sign;
+  } else if (ex == 31) {
+    u = sign | 0x7F800000u | (man << 13);
+  } else {
+    u = sign | ((ex + 112u) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+/* A sparse-attention operand element: bf16 (f16 = 0) or fp16 (f16 = 1) bits. */
+static inline double elem(uint16_t b, int f16) { return f16 ? (double)f16_to_f32(b) : (double)bf16_to_f32(b); }
+
+void oracle_f16_to_f32(const uint16_t* h, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(h[i]);
+}
+
 /*
  * Scores of `nrows` query rows against the keys of one batch.
  *   q   [S, H, D] bf16 bits       k [T, D] bf16 bits       w [S, H] fp32
@@ -189,14 +217,15 @@ void oracle_topk(const double* scores, int64_t nrows, int64_t T, const int64_t* 
 /*
  * Sparse attention with attention sink, MQA layout (reference.py:93-130), for
  * `nrows` query rows of one batch.
- *   q [nrows, H, D] bf16 bits; kv [N, D] bf16 bits; sink [H] fp32;
- *   idx [nrows, K] int64 (-1 = masked).  Out: o [nrows, H, D], lse [nrows, H].
+ *   q [nrows, H, D], kv [N, D]: bf16 bits (f16 = 0) or fp16 bits (f16 = 1);
+ *   sink [H] fp32; idx [nrows, K] int64 (-1 = masked).  Out: o [nrows, H, D],
+ *   lse [nrows, H].
  * The sink enters the denominator only.  LSE = log(sum) + max as in
  * sparse_attn_fwd.py:174-177 (sink included in the sum).
  */
-void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink, const int64_t* idx,
-                        int64_t nrows, int64_t H, int64_t D, int64_t N, int64_t K, double scale,
-                        double* o, double* lse) {
+void oracle_sparse_attn_t(const uint16_t* q, const uint16_t* kv, const float* sink, const int64_t* idx,
+                          int64_t nrows, int64_t H, int64_t D, int64_t N, int64_t K, double scale, int f16,
+                          double* o, double* lse) {
 #pragma omp parallel
   {
     double* sc = (double*)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
@@ -206,7 +235,7 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
       const int64_t* ir = idx + r * K;
       for (int64_t h = 0; h < H; ++h) {
         const uint16_t* qh = q + (r * H + h) * D;
-        for (int64_t d = 0; d < D; ++d) qd[d] = (double)bf16_to_f32(qh[d]);
+        for (int64_t d = 0; d < D; ++d) qd[d] = elem(qh[d], f16);
         double mx = (double)sink[h];
         for (int64_t j = 0; j < K; ++j) {
           const int64_t t = ir[j];
@@ -216,7 +245,7 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
           }
           const uint16_t* kr = kv + t * D;
           double dot = 0.0;
-          for (int64_t d = 0; d < D; ++d) dot += qd[d] * (double)bf16_to_f32(kr[d]);
+          for (int64_t d = 0; d < D; ++d) dot += qd[d] * elem(kr[d], f16);
           sc[j] = dot * scale;
           if (sc[j] > mx) mx = sc[j];
         }
@@ -234,7 +263,7 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
           const double p = exp(sc[j] - mx);
           den += p;
           const uint16_t* kr = kv + ir[j] * D;
-          for (int64_t d = 0; d < D; ++d) oh[d] += p * (double)bf16_to_f32(kr[d]);
+          for (int64_t d = 0; d < D; ++d) oh[d] += p * elem(kr[d], f16);
         }
         for (int64_t d = 0; d < D; ++d) oh[d] /= den;
         lse[r * H + h] = log(den) + mx;
@@ -245,6 +274,12 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
   }
 }
 
+void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink, const int64_t* idx,
+                        int64_t nrows, int64_t H, int64_t D, int64_t N, int64_t K, double scale,
+                        double* o, double* lse) {
+  oracle_sparse_attn_t(q, kv, sink, idx, nrows, H, D, N, K, scale, 0, o, lse);
+}
+
 /*
  * Sparse-attention backward for `nrows` query rows of one batch, from the
  * forward's saved outputs, as the reference backward consumes them:
@@ -253,7 +288,7 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
  *   gradients  sparse_attn_bwd.py:247-283 (p = exp(s - lse), dp = p (do.v - delta) scale,
  *              dq = dp.kv, dkv[idx] += dp^T q + p^T do)
  *   dsink      sparse_attn_bwd.py:224-228 (-exp(sink - lse) delta, summed over rows)
- *   q, o, dout [nrows,H,D] bf16 bits; kv [N,D] bf16 bits; sink [H] fp32;
+ *   q, o, dout [nrows,H,D], kv [N,D]: bf16 bits (f16 = 0) or fp16 bits (f16 = 1); sink [H] fp32;
  *   lse [nrows,H] fp32; idx [nrows,K] int64 (-1 or out of range = masked).
  * Outputs, each optional (NULL = not wanted):
  *   dq    [nrows,H,D]  written;
@@ -263,10 +298,10 @@ void oracle_sparse_attn(const uint16_t* q, const uint16_t* kv, const float* sink
  * A key listed twice in a row contributes twice, as the reference's
  * per-slot atomic adds do.  All sums in double.
  */
-void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_t* o, const uint16_t* dout,
-                            const float* sink, const float* lse, const int64_t* idx, int64_t nrows, int64_t H,
-                            int64_t D, int64_t N, int64_t K, double scale, const int64_t* key_slot, int64_t nslot,
-                            double* dq, double* dkv, double* dsink) {
+void oracle_sparse_attn_bwd_t(const uint16_t* q, const uint16_t* kv, const uint16_t* o, const uint16_t* dout,
+                              const float* sink, const float* lse, const int64_t* idx, int64_t nrows, int64_t H,
+                              int64_t D, int64_t N, int64_t K, double scale, const int64_t* key_slot, int64_t nslot,
+                              int f16, double* dq, double* dkv, double* dsink) {
   const int pairs = dq != NULL || (dkv != NULL && nslot > 0);
 #pragma omp parallel
   {
@@ -283,12 +318,12 @@ void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_
         const double l = (double)lse[rh];
         double delta = 0.0;
         for (int64_t d = 0; d < D; ++d)
-          delta += (double)bf16_to_f32(o[rh * D + d]) * (double)bf16_to_f32(dout[rh * D + d]);
+          delta += elem(o[rh * D + d], f16) * elem(dout[rh * D + d], f16);
         my_ds[h] -= exp((double)sink[h] - l) * delta;
         if (!pairs) continue;
         for (int64_t d = 0; d < D; ++d) {
-          qd[d] = (double)bf16_to_f32(q[rh * D + d]);
-          gd[d] = (double)bf16_to_f32(dout[rh * D + d]);
+          qd[d] = elem(q[rh * D + d], f16);
+          gd[d] = elem(dout[rh * D + d], f16);
         }
         double* dqh = dq ? dq + rh * D : NULL;
         if (dqh) for (int64_t d = 0; d < D; ++d) dqh[d] = 0.0;
@@ -300,7 +335,7 @@ void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_
           const uint16_t* kr = kv + t * D;
           double qk = 0.0, gk = 0.0;
           for (int64_t d = 0; d < D; ++d) {
-            kd[d] = (double)bf16_to_f32(kr[d]);
+            kd[d] = elem(kr[d], f16);
             qk += qd[d] * kd[d];
             gk += gd[d] * kd[d];
           }
@@ -327,4 +362,12 @@ void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_
     free(my_dkv);
     free(my_ds);
   }
+}
+
+void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_t* o, const uint16_t* dout,
+                            const float* sink, const float* lse, const int64_t* idx, int64_t nrows, int64_t H,
+                            int64_t D, int64_t N, int64_t K, double scale, const int64_t* key_slot, int64_t nslot,
+                            double* dq, double* dkv, double* dsink) {
+  oracle_sparse_attn_bwd_t(q, kv, o, dout, sink, lse, idx, nrows, H, D, N, K, scale, key_slot, nslot, 0, dq, dkv,
+                           dsink);
 }

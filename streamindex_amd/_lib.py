@@ -43,10 +43,10 @@ SIGNATURES = {
     "si_csa_scores_topk": (_I32, [_P, _I64P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P]),
     "si_hca_topk_idxs": (_I32, [_I64, _I64, _I64, _I64, _I64, _I64, _P, _I64P, _P]),
     "si_sparse_attn_fwd": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P,
-                                  _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                  _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                   _P, _I64P, _P, _I64P, _P]),
     "si_sparse_attn_fwd_ragged": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P,
-                                         _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                         _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                          _P, _I64P, _P, _I64P, _P, _I64P, _P]),
     "si_indexer_topk_q": (_I32, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I32, _I64P, _P, _I64P,
                                  _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
@@ -60,14 +60,14 @@ SIGNATURES = {
     "si_gated_pool": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _P]),
     "si_sparse_attn_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "si_sparse_attn_bwd": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
-                                  _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                  _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                   _P, _I64P, _P, _I64P, _P, _P, _I64, _P]),
     "si_sparse_attn_bwd_ragged": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
-                                         _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                         _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                          _P, _I64P, _P, _I64P, _P, _P, _I64, _P, _I64P, _P]),
     "si_sparse_attn_bwd_noalloc_scratch_bytes": (_I64, []),
     "si_sparse_attn_bwd_noalloc": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
-                                          _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+                                          _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                           _P, _I64P, _P, _I64P, _P, _P, _I64P, _P]),
 }
 
@@ -107,6 +107,19 @@ def strides(t: torch.Tensor):
 
 def int64s(*vals):
     return (ctypes.c_int64 * len(vals))(*vals)
+
+
+SI_DTYPE_BF16 = 0
+SI_DTYPE_F16 = 1
+
+
+def qkv_dtype(t: torch.Tensor) -> int:
+    """C-ABI element-type code of a sparse-attention operand (bf16 or fp16)."""
+    if t.dtype == torch.bfloat16:
+        return SI_DTYPE_BF16
+    if t.dtype == torch.float16:
+        return SI_DTYPE_F16
+    raise ValueError(f"sparse attention operands must be bfloat16 or float16, got {t.dtype}")
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -102,6 +102,54 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+// ---------------------------------------------------------------------------
+// The 16-bit element type of q / kv / o (and of the backward's dO, dq, dkv and
+// its bf16 coefficient tiles): F16 = false is bf16, true is fp16.  Operands
+// travel as raw 16-bit lanes (bf16x8 / uint32 pairs) and are reinterpreted at
+// the MFMA and at the conversions.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// D += A * B over 16x16x32 tiles in the element type (fp32 accumulate).
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  if constexpr (F16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+}
+
+// Two floats to two packed elements, round-to-nearest-even.
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (F16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  } else {
+    return f32x2_to_bf16x2(a, b);
+  }
+}
+
+// The low / high element of a packed pair, widened to fp32 (exact).
+template <bool F16>
+__device__ __forceinline__ float elem_lo(uint32_t w) {
+  if constexpr (F16) {
+    return static_cast<float>(__builtin_bit_cast(f16x2, w)[0]);
+  } else {
+    return __uint_as_float(w << 16);
+  }
+}
+template <bool F16>
+__device__ __forceinline__ float elem_hi(uint32_t w) {
+  if constexpr (F16) {
+    return static_cast<float>(__builtin_bit_cast(f16x2, w)[1]);
+  } else {
+    return __uint_as_float(w & 0xffff0000u);
+  }
+}
+
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
 template <int I, int N, typename F>
 __device__ __forceinline__ void attn_static_for(F&& f) {

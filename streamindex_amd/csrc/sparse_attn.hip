@@ -49,15 +49,15 @@
 namespace si {
 
 struct SparseAttnArgs {
-  const uint16_t* q;  // [B,S,H,D] bf16
+  const uint16_t* q;  // [B,S,H,D] bf16 or fp16 (f16)
   int64_t qsb, qss, qsh;
-  const uint16_t* kv;  // [B,N,D] bf16
+  const uint16_t* kv;  // [B,N,D], q's type
   int64_t kvsb, kvsn;
   const float* sink;   // [H]
   const void* idx;     // [B,S,K] int32 / int64
   int idx64;
   int64_t isb, iss, isk;
-  uint16_t* o;         // [B,S,H,D] bf16
+  uint16_t* o;         // [B,S,H,D], q's type
   int64_t osb, oss, osh;
   float* lse;          // [B,S,H]
   int64_t lsb, lss, lsh;
@@ -66,6 +66,7 @@ struct SparseAttnArgs {
   int64_t rlsb, rlss;
   int HG;              // head groups of 64
   float scale_log2;    // softmax_scale * log2(e)
+  int f16;             // element type: 0 bf16, 1 fp16
 };
 
 // The reference maximum of a head moves only when a tile's maximum exceeds it
@@ -73,13 +74,16 @@ struct SparseAttnArgs {
 // the fp32/bf16 exponent range, and the output accumulator is rescaled only
 // on such a jump.  (Up to rounding the result equals the eager rescale.)
 constexpr float kLazyRescale = 64.0f;
+// With fp16 operands P = 2^(x - m_ref) must stay inside the fp16 range
+// (max 65504): the reference moves once a tile's maximum exceeds it by 2^8.
+constexpr float kLazyRescaleF16 = 8.0f;
 
 // Threads of a workgroup: kAttnWaves S^T / softmax waves ("producers", 16
 // heads each) and kAttnWaves P.V waves ("consumers", 16-dim output blocks
 // dealt round-robin), one of each per SIMD.
 constexpr int kAttnThreads = 2 * kAttnWaves * 64;
 
-template <int D, bool IDX64>
+template <int D, bool IDX64, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
   using SH = AttnShape<D>;
   constexpr int KS = SH::KS;
@@ -213,8 +217,8 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         constexpr int ks = decltype(KC)::value;
         constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
         lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
-        st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
-        st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
+        st[0] = mfma16x16x32<F16>(kq[ks % QPD][0], qf[ks], st[0]);
+        st[1] = mfma16x16x32<F16>(kq[ks % QPD][1], qf[ks], st[1]);
         if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
       };
       attn_static_for<0, KS>(qk_step);
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       // First valid key of the head: the accumulator and denominator are
       // still zero, so the reference moves without a rescale (alpha = 1).
       const bool first = m_ref == -1.0e30f;
-      const bool raise = first ? tmax > m_ref : tmax > m_ref + kLazyRescale;
+      const bool raise = first ? tmax > m_ref : tmax > m_ref + (F16 ? kLazyRescaleF16 : kLazyRescale);
       const float m_new = raise ? tmax : m_ref;
       out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
       m_ref = m_new;
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       l_run = l_run * out.alpha + psum;
       // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
 #pragma unroll
-      for (int c = 0; c < 4; ++c) out.w[c] = f32x2_to_bf16x2(p[c][0], p[c][1]);
+      for (int c = 0; c < 4; ++c) out.w[c] = pack2<F16>(p[c][0], p[c][1]);
       return out;
     };
     // (inline asm: the compiler makes a tracked LDS access that follows
@@ -445,7 +449,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         }
         const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j & 1], hi[j & 1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pbr[nb], oacc[j][nb], 0, 0, 0);
+        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = mfma16x16x32<F16>(vf, pbr[nb], oacc[j][nb]);
         if constexpr (j + 2 < MBW) {
           lo[j & 1] = tr_read<128 * (j + 2)>(ta);
           hi[j & 1] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
@@ -512,8 +516,8 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
           uint2 w;
-          w.x = f32x2_to_bf16x2(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
-          w.y = f32x2_to_bf16x2(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
+          w.x = pack2<F16>(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
+          w.y = pack2<F16>(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
           *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
         }
       }
@@ -535,12 +539,13 @@ template <int D>
 static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
   const int64_t nblk = static_cast<int64_t>(a.B) * a.S * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  if (a.idx64) {
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnThreads),
-                       0, st, a);
+  const dim3 grid(static_cast<unsigned>(nblk)), block(kAttnThreads);
+  if (a.f16) {
+    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, true>), grid, block, 0, st, a);
   } else {
-    hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false>), dim3(static_cast<unsigned>(nblk)), dim3(kAttnThreads),
-                       0, st, a);
+    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, false>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, false>), grid, block, 0, st, a);
   }
   return check_launch("sparse_attn_fwd_kernel");
 }
@@ -552,10 +557,12 @@ using namespace si;
 extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv,
                                          const int64_t* kv_strides, const float* attn_sink, const void* topk_idxs,
                                          int idx_is_i64, const int64_t* idx_strides, int64_t B, int64_t S, int64_t H,
-                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* o,
-                                         const int64_t* o_strides, float* lse, const int64_t* lse_strides,
+                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype,
+                                         void* o, const int64_t* o_strides, float* lse, const int64_t* lse_strides,
                                          const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
   if (row_len && !row_len_strides) return set_error(SI_ERR_INVALID, "null row_len strides");
+  if (qkv_dtype != SI_DTYPE_BF16 && qkv_dtype != SI_DTYPE_F16)
+    return set_error(SI_ERR_INVALID, "qkv_dtype must be SI_DTYPE_BF16 (0) or SI_DTYPE_F16 (1)");
   if (!q_strides || !kv_strides || !idx_strides || !o_strides || !lse_strides)
     return set_error(SI_ERR_INVALID, "null stride argument");
   if (B < 0 || S < 0 || H <= 0 || D <= 0 || N_kv < 0 || K < 0) return set_error(SI_ERR_INVALID, "bad dimension");
@@ -599,6 +606,7 @@ extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides
   }
   a.HG = static_cast<int>((H + 63) / 64);
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.f16 = qkv_dtype == SI_DTYPE_F16 ? 1 : 0;
   if (a.B == 0 || a.S == 0) return SI_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (D) {
@@ -617,9 +625,9 @@ extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides
 extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
                                   const float* attn_sink, const void* topk_idxs, int idx_is_i64,
                                   const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D,
-                                  int64_t N_kv, int64_t K, float softmax_scale, void* o, const int64_t* o_strides,
-                                  float* lse, const int64_t* lse_strides, void* stream) {
+                                  int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype, void* o,
+                                  const int64_t* o_strides, float* lse, const int64_t* lse_strides, void* stream) {
   return si_sparse_attn_fwd_ragged(q, q_strides, kv, kv_strides, attn_sink, topk_idxs, idx_is_i64, idx_strides, B, S,
-                                   H, D, N_kv, K, softmax_scale, o, o_strides, lse, lse_strides, nullptr, nullptr,
-                                   stream);
+                                   H, D, N_kv, K, softmax_scale, qkv_dtype, o, o_strides, lse, lse_strides, nullptr,
+                                   nullptr, stream);
 }

@@ -47,31 +47,32 @@
 namespace si {
 
 struct AttnBwdArgs {
-  const uint16_t* q;  // [B,S,H,D] bf16
+  const uint16_t* q;  // [B,S,H,D] bf16 or fp16 (f16); kv, o, dout, dq, coef and prow share the type
   int64_t qsb, qss, qsh;
-  const uint16_t* kv;  // [B,N,D] bf16
+  const uint16_t* kv;  // [B,N,D]
   int64_t kvsb, kvsn;
   const float* sink;   // [H]
   const void* idx;     // [B,S,K] int32 / int64
   int idx64;
   int64_t isb, iss, isk;
-  const uint16_t* o;   // [B,S,H,D] bf16, forward output
+  const uint16_t* o;   // [B,S,H,D], forward output
   int64_t osb, oss, osh;
-  const uint16_t* dout;  // [B,S,H,D] bf16, gradient of o
+  const uint16_t* dout;  // [B,S,H,D], gradient of o
   int64_t gsb, gss, gsh;
   const float* lse;    // [B,S,H]
   int64_t lsb, lss, lsh;
-  uint16_t* dq;        // [B,S,H,D] bf16
+  uint16_t* dq;        // [B,S,H,D]
   int64_t dqsb, dqss, dqsh;
   float* dsink_rows;   // [B*S, 64*HG]: -e^{sink-lse} delta per (row, head)
-  uint16_t* coef;      // [nrows, HG, ntiles, 2, 4, 64, 8] bf16: P, dS fragments
-  uint16_t* prow;      // [nrows, HG, 32 ntiles, D] bf16: per-(query, slot) dkv rows
+  uint16_t* coef;      // [nrows, HG, ntiles, 2, 4, 64, 8]: P, dS fragments
+  uint16_t* prow;      // [nrows, HG, 32 ntiles, D]: per-(query, slot) dkv rows
   int B, S, H, N, K, HG, ntiles;  // ntiles: key tiles of a full row (the workspace layout)
   const int32_t* row_len;  // optional [B,S]: columns at or past row_len[b,s] are masked, their tiles skipped
   int64_t rlsb, rlss;
   int64_t row0;        // first global row (b*S + s) of this chunk
   int nrows;           // rows in this chunk
   float scale, scale_log2;
+  int f16;             // element type: 0 bf16, 1 fp16
 };
 
 constexpr int kBwdThreads = 2 * kAttnWaves * 64;
@@ -86,13 +87,11 @@ __device__ __forceinline__ int bwd_row_len(const AttnBwdArgs& a, int b, int s) {
 constexpr int kCoefTile = 2 * kAttnWaves * 64 * 8;
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // ---------------------------------------------------------------------------
 // 1. dQ, P / dS coefficients and dsink terms per query row
 // ---------------------------------------------------------------------------
-template <int D, bool IDX64>
+template <int D, bool IDX64, bool F16>
 __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnBwdArgs a) {
   using SH = AttnShape<D>;
   constexpr int KS = SH::KS;
@@ -150,8 +149,8 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
         const u32x4 gv = __builtin_bit_cast(u32x4, gf[ks]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          delta = __builtin_fmaf(bf_lo(ov[c]), bf_lo(gv[c]), delta);
-          delta = __builtin_fmaf(bf_hi(ov[c]), bf_hi(gv[c]), delta);
+          delta = __builtin_fmaf(elem_lo<F16>(ov[c]), elem_lo<F16>(gv[c]), delta);
+          delta = __builtin_fmaf(elem_hi<F16>(ov[c]), elem_hi<F16>(gv[c]), delta);
         }
       }
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(delta), __float_as_uint(delta), false, false);
@@ -195,10 +194,10 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
         constexpr int ks = decltype(KC)::value;
         constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);
         lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
-        st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], qf[ks], st[0], 0, 0, 0);
-        dp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][0], gf[ks], dp[0], 0, 0, 0);
-        st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], qf[ks], st[1], 0, 0, 0);
-        dp[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kq[ks % QPD][1], gf[ks], dp[1], 0, 0, 0);
+        st[0] = mfma16x16x32<F16>(kq[ks % QPD][0], qf[ks], st[0]);
+        dp[0] = mfma16x16x32<F16>(kq[ks % QPD][0], gf[ks], dp[0]);
+        st[1] = mfma16x16x32<F16>(kq[ks % QPD][1], qf[ks], st[1]);
+        dp[1] = mfma16x16x32<F16>(kq[ks % QPD][1], gf[ks], dp[1]);
         if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
       };
       attn_static_for<0, KS>(qk_step);
@@ -223,8 +222,8 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
       u32x4 wp, wd;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        wp[c] = f32x2_to_bf16x2(p[c >> 1][2 * (c & 1)], p[c >> 1][2 * (c & 1) + 1]);
-        wd[c] = f32x2_to_bf16x2(d[c >> 1][2 * (c & 1)], d[c >> 1][2 * (c & 1) + 1]);
+        wp[c] = pack2<F16>(p[c >> 1][2 * (c & 1)], p[c >> 1][2 * (c & 1) + 1]);
+        wd[c] = pack2<F16>(d[c >> 1][2 * (c & 1)], d[c >> 1][2 * (c & 1) + 1]);
       }
       const uint32_t pa = lds_addr(&p_lds[t & 1][(wave * 64 + lane) * 16]);
       asm volatile("ds_write_b128 %0, %1" ::"v"(pa), "v"(wd) : "memory");
@@ -367,7 +366,7 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
         }
         const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j & 1], hi[j & 1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) qacc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pbr[nb], qacc[j][nb], 0, 0, 0);
+        for (int nb = 0; nb < 4; ++nb) qacc[j][nb] = mfma16x16x32<F16>(vf, pbr[nb], qacc[j][nb]);
         if constexpr (j + 2 < MBW) {
           lo[j & 1] = tr_read<128 * (j + 2)>(ta);
           hi[j & 1] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
@@ -435,8 +434,8 @@ __global__ __launch_bounds__(kBwdThreads) void sparse_attn_bwd_rows_kernel(AttnB
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
           uint2 w;
-          w.x = f32x2_to_bf16x2(qacc[j][nb][0], qacc[j][nb][1]);
-          w.y = f32x2_to_bf16x2(qacc[j][nb][2], qacc[j][nb][3]);
+          w.x = pack2<F16>(qacc[j][nb][0], qacc[j][nb][1]);
+          w.y = pack2<F16>(qacc[j][nb][2], qacc[j][nb][3]);
           *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
         }
       }
@@ -473,7 +472,7 @@ struct DkvShape {
 // 16x16x32 A-fragment holds 8 heads of one dimension and a B-fragment lane 8
 // heads of one key: both come from two ds_read_b64_tr_b16 (a 16-lane group
 // reads a 4 x 16 block and each lane receives one column of 4).
-template <int D>
+template <int D, bool F16>
 __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(AttnBwdArgs a) {
   using DS = DkvShape<D>;
   constexpr int MBW = DS::MBW;
@@ -611,8 +610,8 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
         for (int kst = 0; kst < 4; ++kst) {
           const bf16x8 af =
               __builtin_bit_cast(bf16x8, __builtin_shufflevector(alo[j & 1][kst], ahi[j & 1][kst], 0, 1, 2, 3, 4, 5, 6, 7));
-          acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[kst][0], acc[0], 0, 0, 0);
-          acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[kst][1], acc[1], 0, 0, 0);
+          acc[0] = mfma16x16x32<F16>(af, bfr[kst][0], acc[0]);
+          acc[1] = mfma16x16x32<F16>(af, bfr[kst][1], acc[1]);
         }
         // lane (key 16nb + i16, g) holds dimensions 16 mbi + 4g + 0..3.  Every
         // slot of the padded tile is written: a masked or padding slot has
@@ -621,8 +620,8 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           uint2 w;
-          w.x = f32x2_to_bf16x2(acc[nb][0], acc[nb][1]);
-          w.y = f32x2_to_bf16x2(acc[nb][2], acc[nb][3]);
+          w.x = pack2<F16>(acc[nb][0], acc[nb][1]);
+          w.y = pack2<F16>(acc[nb][2], acc[nb][3]);
           *reinterpret_cast<uint2*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + mbi * 16 + 4 * g) = w;
         }
       }
@@ -667,7 +666,7 @@ struct ReduceShape {
   static constexpr int NT = 256;
 };
 
-template <int D>
+template <int D, bool F16>
 __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce_kernel(DkvReduceArgs r) {
   constexpr int CPR = ReduceShape<D>::CPR;    // 16-byte chunks per row
   constexpr int G = ReduceShape<D>::G;        // pair groups
@@ -689,8 +688,8 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
         const u32x4 v = *reinterpret_cast<const u32x4*>(r.prow + ((lrow * r.HG + h) * r.KP + j) * D + c * 8);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sum[2 * e] += bf_lo(v[e]);
-          sum[2 * e + 1] += bf_hi(v[e]);
+          sum[2 * e] += elem_lo<F16>(v[e]);
+          sum[2 * e + 1] += elem_hi<F16>(v[e]);
         }
       }
     };
@@ -713,8 +712,8 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
           for (int u = 0; u < 8; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              sum[2 * e] += bf_lo(v[u][e]);
-              sum[2 * e + 1] += bf_hi(v[u][e]);
+              sum[2 * e] += elem_lo<F16>(v[u][e]);
+              sum[2 * e + 1] += elem_hi<F16>(v[u][e]);
             }
         }
       } else {
@@ -751,7 +750,7 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
       const int b = kid / r.N, t = kid % r.N;
       u32x4 w;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = f32x2_to_bf16x2(tot[2 * e], tot[2 * e + 1]);
+      for (int e = 0; e < 4; ++e) w[e] = pack2<F16>(tot[2 * e], tot[2 * e + 1]);
       *reinterpret_cast<u32x4*>(r.dkv + b * r.dsb + static_cast<int64_t>(t) * r.dsn + c * 8) = w;
     }
   }
@@ -900,7 +899,7 @@ static int bwd_rows_for(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, i
   return bwd_plan(B, S, H, D, N, K, lo, out);
 }
 
-template <int D>
+template <int D, bool F16>
 static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_rows, uint16_t* dkv, int64_t dkvsb,
                       int64_t dkvsn, float* dsink, hipStream_t st) {
   const int64_t nkeys = static_cast<int64_t>(a.B) * a.N;
@@ -930,9 +929,9 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     a.nrows = static_cast<int>(nr);
     const unsigned grid = static_cast<unsigned>(nr * a.HG);
     if (a.idx64)
-      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, true>), dim3(grid), dim3(kBwdThreads), 0, st, a);
+      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, true, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
     else
-      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, false>), dim3(grid), dim3(kBwdThreads), 0, st, a);
+      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, false, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
     if ((rc = check_launch("sparse_attn_bwd_rows_kernel"))) return rc;
     if (a.ntiles == 0) continue;
     const int64_t npairs = nr * a.K;
@@ -955,7 +954,7 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     hipLaunchKernelGGL(sparse_attn_bwd_segments_kernel, dim3(pblocks), dim3(256), 0, st, kout, npairs,
                        static_cast<uint32_t>(nkeys), seg_lo, seg_hi);
     if ((rc = check_launch("sparse_attn_bwd_segments_kernel"))) return rc;
-    hipLaunchKernelGGL((sparse_attn_bwd_dkv_rows_kernel<D>), dim3(grid), dim3(kRowsThreads), 0, st, a);
+    hipLaunchKernelGGL((sparse_attn_bwd_dkv_rows_kernel<D, F16>), dim3(grid), dim3(kRowsThreads), 0, st, a);
     if ((rc = check_launch("sparse_attn_bwd_dkv_rows_kernel"))) return rc;
     DkvReduceArgs r{};
     r.pair = vout;
@@ -972,7 +971,7 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
     r.N = a.N;
     r.first = row0 == 0;
     r.last = row0 + nr >= total_rows;
-    hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D>), dim3(static_cast<unsigned>(nkeys)),
+    hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D, F16>), dim3(static_cast<unsigned>(nkeys)),
                        dim3(ReduceShape<D>::NT), 0, st, r);
     if ((rc = check_launch("sparse_attn_bwd_dkv_reduce_kernel"))) return rc;
   }
@@ -1069,11 +1068,13 @@ extern "C" int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides
                                          int idx_is_i64, const int64_t* idx_strides, const void* o,
                                          const int64_t* o_strides, const float* lse, const int64_t* lse_strides,
                                          const void* dout, const int64_t* do_strides, int64_t B, int64_t S, int64_t H,
-                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, void* dq,
-                                         const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
+                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype,
+                                         void* dq, const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
                                          float* dsink, void* workspace, int64_t workspace_bytes,
                                          const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
   if (row_len && !row_len_strides) return set_error(SI_ERR_INVALID, "null row_len strides");
+  if (qkv_dtype != SI_DTYPE_BF16 && qkv_dtype != SI_DTYPE_F16)
+    return set_error(SI_ERR_INVALID, "qkv_dtype must be SI_DTYPE_BF16 (0) or SI_DTYPE_F16 (1)");
   if (!q_strides || !kv_strides || !idx_strides || !o_strides || !lse_strides || !do_strides || !dq_strides ||
       !dkv_strides)
     return set_error(SI_ERR_INVALID, "null stride argument");
@@ -1137,17 +1138,23 @@ extern "C" int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides
   a.scale = softmax_scale;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.idx64 = idx_is_i64 ? 1 : 0;
+  a.f16 = qkv_dtype == SI_DTYPE_F16 ? 1 : 0;
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* dkvp = static_cast<uint16_t*>(dkv);
   const int64_t total_rows = B * S;
+  auto run = [&](auto DC) {
+    constexpr int DD = decltype(DC)::value;
+    return a.f16 ? launch_bwd<DD, true>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st)
+                 : launch_bwd<DD, false>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
+  };
   switch (D) {
-    case 32: return launch_bwd<32>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
-    case 64: return launch_bwd<64>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
-    case 128: return launch_bwd<128>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
-    case 256: return launch_bwd<256>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
-    case 512: return launch_bwd<512>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
-    default: return launch_bwd<576>(a, pl, ws, total_rows, dkvp, dkv_strides[0], dkv_strides[1], dsink, st);
+    case 32: return run(std::integral_constant<int, 32>{});
+    case 64: return run(std::integral_constant<int, 64>{});
+    case 128: return run(std::integral_constant<int, 128>{});
+    case 256: return run(std::integral_constant<int, 256>{});
+    case 512: return run(std::integral_constant<int, 512>{});
+    default: return run(std::integral_constant<int, 576>{});
   }
 }
 
@@ -1156,12 +1163,13 @@ extern "C" int si_sparse_attn_bwd(const void* q, const int64_t* q_strides, const
                                   const int64_t* idx_strides, const void* o, const int64_t* o_strides, const float* lse,
                                   const int64_t* lse_strides, const void* dout, const int64_t* do_strides, int64_t B,
                                   int64_t S, int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale,
-                                  void* dq, const int64_t* dq_strides, void* dkv, const int64_t* dkv_strides,
-                                  float* dsink, void* workspace, int64_t workspace_bytes, void* stream) {
+                                  int qkv_dtype, void* dq, const int64_t* dq_strides, void* dkv,
+                                  const int64_t* dkv_strides, float* dsink, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
   return si_sparse_attn_bwd_ragged(q, q_strides, kv, kv_strides, attn_sink, topk_idxs, idx_is_i64, idx_strides, o,
                                    o_strides, lse, lse_strides, dout, do_strides, B, S, H, D, N_kv, K, softmax_scale,
-                                   dq, dq_strides, dkv, dkv_strides, dsink, workspace, workspace_bytes, nullptr,
-                                   nullptr, stream);
+                                   qkv_dtype, dq, dq_strides, dkv, dkv_strides, dsink, workspace, workspace_bytes,
+                                   nullptr, nullptr, stream);
 }
 
 static int inv_check(int64_t B, int64_t S, int64_t K, int64_t N, int64_t k_max) {

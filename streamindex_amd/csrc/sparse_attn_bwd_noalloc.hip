@@ -59,7 +59,7 @@ extern "C" int si_sparse_attn_bwd_noalloc(const void* q, const int64_t* q_stride
                                           const int64_t* o_strides, const float* lse, const int64_t* lse_strides,
                                           const void* dout, const int64_t* do_strides, int64_t B, int64_t S,
                                           int64_t H, int64_t D, int64_t N_kv, int64_t K, float softmax_scale,
-                                          void* dq, const int64_t* dq_strides, void* dkv,
+                                          int qkv_dtype, void* dq, const int64_t* dq_strides, void* dkv,
                                           const int64_t* dkv_strides, float* dsink, const int32_t* row_len,
                                           const int64_t* row_len_strides, void* stream) {
   // What the plan for this problem needs within the scratch: its whole
@@ -77,6 +77,6 @@ extern "C" int si_sparse_attn_bwd_noalloc(const void* q, const int64_t* q_stride
   if (rc) return rc;
   return si_sparse_attn_bwd_ragged(q, q_strides, kv, kv_strides, attn_sink, topk_idxs, idx_is_i64, idx_strides, o,
                                    o_strides, lse, lse_strides, dout, do_strides, B, S, H, D, N_kv, K, softmax_scale,
-                                   dq, dq_strides, dkv, dkv_strides, dsink, ws, kNoAllocScratchBytes, row_len,
+                                   qkv_dtype, dq, dq_strides, dkv, dkv_strides, dsink, ws, kNoAllocScratchBytes, row_len,
                                    row_len_strides, stream);
 }

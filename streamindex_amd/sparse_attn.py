@@ -15,8 +15,8 @@ Differences, all deliberate:
   of bounds.
 * The backward reduces dkv deterministically (per-(query, slot) rows
   reduced key by key in a fixed order) instead of with fp32 atomics, so
-  repeated calls give bit-identical gradients; each row is rounded to bf16
-  before the fp32 sum.  Its workspace comes from the torch caching allocator
+  repeated calls give bit-identical gradients; each row is rounded to the
+  operand type (bf16 or fp16) before the fp32 sum.  Its workspace comes from the torch caching allocator
   and long sequences are processed in chunks of query rows that fit it.
 """
 
@@ -56,7 +56,7 @@ def sparse_attn_fwd(
     """MQA sparse attention with attention sink.
 
     Args:
-      q: ``[B, S, H, D]`` bf16.  kv: ``[B, N_kv, D]`` bf16 (one shared head).
+      q: ``[B, S, H, D]`` bf16 or fp16.  kv: ``[B, N_kv, D]`` of q's type (one shared head).
       attn_sink: ``[H]`` fp32.  topk_idxs: ``[B, S, K]`` int32/int64, ``-1`` = masked.
       softmax_scale: defaults to ``D ** -0.5``.
       row_len: optional ``[B, S]`` int32 (an extension, not in the reference):
@@ -64,7 +64,7 @@ def sparse_attn_fwd(
         never gathered or computed.  For rows whose tail is already ``-1``
         (HCA, short CSA rows) the result is unchanged and the tail costs nothing.
     Returns:
-      ``(o [B,S,H,D] bf16, lse [B,S,H] fp32)``.  A row with no valid index
+      ``(o [B,S,H,D] in q's type, lse [B,S,H] fp32)``.  A row with no valid index
       gets ``o = 0`` and ``lse = sink`` (or ``-1e30`` if the sink is ``-inf``).
     """
     del block_h, block_n
@@ -80,8 +80,6 @@ def sparse_attn_fwd(
     assert attn_sink.shape == (H,)
     assert topk_idxs.shape[:2] == (B, S)
     assert topk_idxs.dim() == 3
-    if q.dtype != torch.bfloat16:
-        raise ValueError("only bfloat16 q/kv are supported on MI355X")
     if D not in SUPPORTED_D:
         raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
     if H > MAX_HEADS:
@@ -111,7 +109,7 @@ def sparse_attn_fwd(
         rc = L.si_sparse_attn_fwd_ragged(
             q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
             topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
-            B, S, H, D, N_kv, K, float(softmax_scale), o.data_ptr(), _lib.strides(o),
+            B, S, H, D, N_kv, K, float(softmax_scale), _lib.qkv_dtype(q), o.data_ptr(), _lib.strides(o),
             lse.data_ptr(), _lib.strides(lse), None if row_len is None else row_len.data_ptr(),
             None if row_len is None else _lib.strides(row_len), _lib.stream_ptr(q.device))
     _lib.check(rc)
@@ -164,8 +162,7 @@ def sparse_attn_bwd(
     assert o.shape == q.shape and o.dtype == q.dtype
     assert lse.shape == (B, S, H) and attn_sink.shape == (H,)
     assert topk_idxs.shape[:2] == (B, S)
-    if q.dtype != torch.bfloat16:
-        raise ValueError("only bfloat16 q/kv are supported on MI355X")
+    assert q.dtype in (torch.bfloat16, torch.float16), f"Q must be bf16 or fp16, got {q.dtype}"
     if D not in SUPPORTED_D:
         raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
     if H > MAX_HEADS:
@@ -197,7 +194,7 @@ def sparse_attn_bwd(
             q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
             topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
             o.data_ptr(), _lib.strides(o), lse.data_ptr(), _lib.strides(lse), do.data_ptr(), _lib.strides(do),
-            B, S, H, D, N_kv, K, float(softmax_scale), dq.data_ptr(), _lib.strides(dq),
+            B, S, H, D, N_kv, K, float(softmax_scale), _lib.qkv_dtype(q), dq.data_ptr(), _lib.strides(dq),
             dkv.data_ptr(), _lib.strides(dkv), dsink.data_ptr(), ws.data_ptr(), ws.numel(),
             None if row_len is None else row_len.data_ptr(), None if row_len is None else _lib.strides(row_len),
             _lib.stream_ptr(q.device))

@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.si_abi_version() == 5
+    assert lib.si_abi_version() == 6
     assert lib.si_indexer_topk_workspace_bytes(1, 1 << 20, 1 << 18, 64, 128, 512) == 0
 
 
@@ -92,8 +92,13 @@ def test_c_validation_codes_without_gpu(lib):
     # sparse attention: unsupported head dim
     o4 = _i64(64 * 100, 64 * 100, 100, 1)
     rc = lib.si_sparse_attn_fwd(fake, o4, fake, _i64(100 * 16, 100, 1), fake, fake, 1, _i64(32, 8, 1),
-                                1, 4, 64, 100, 16, 8, 0.1, fake, o4, fake, _i64(256, 64, 1), None)
+                                1, 4, 64, 100, 16, 8, 0.1, 0, fake, o4, fake, _i64(256, 64, 1), None)
     assert rc == _lib.SI_ERR_INVALID or rc == _lib.SI_ERR_UNSUPPORTED
+    # sparse attention: element types other than bf16 (0) and fp16 (1)
+    q4 = _i64(64 * 128, 64 * 128, 128, 1)
+    rc = lib.si_sparse_attn_fwd(fake, q4, fake, _i64(100 * 128, 128, 1), fake, fake, 1, _i64(32, 8, 1),
+                                1, 4, 64, 128, 16, 8, 0.1, 2, fake, q4, fake, _i64(256, 64, 1), None)
+    assert rc == _lib.SI_ERR_INVALID and b"qkv_dtype" in lib.si_last_error()
     # empty problems succeed without touching memory
     rc = lib.si_indexer_topk(None, qs, fake, ks, None, 0, ws, None, None, 1, 0, 4, 64, 128, 4, 4, None, None, None)
     assert rc == _lib.SI_OK

@@ -189,7 +189,7 @@ def test_bwd_chunked_workspace(cuda_device):
         rc = L.load().si_sparse_attn_bwd(
             q.data_ptr(), L.strides(q), kv.data_ptr(), L.strides(kv), sink.data_ptr(), idx.data_ptr(), 0,
             L.strides(idx), o.data_ptr(), L.strides(o), lse.data_ptr(), L.strides(lse), do.data_ptr(), L.strides(do),
-            B, S, H, D, N, K, D ** -0.5, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
+            B, S, H, D, N, K, D ** -0.5, 0, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
             dsink.data_ptr(), ws.data_ptr(), 16, L.stream_ptr(q.device))
         L.check(rc)
 
@@ -231,7 +231,7 @@ def test_bwd_no_query_rows_zeroes_dkv(cuda_device):
     rc = lib.si_sparse_attn_bwd(
         q.data_ptr(), L.strides(q), kv.data_ptr(), L.strides(kv), sink.data_ptr(), idx.data_ptr(), 0,
         L.strides(idx), o.data_ptr(), L.strides(o), lse.data_ptr(), L.strides(lse), do.data_ptr(), L.strides(do),
-        1, 0, H, D, N, K, D ** -0.5, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
+        1, 0, H, D, N, K, D ** -0.5, 0, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
         dsink.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_ptr(q.device))
     L.check(rc)
     torch.cuda.synchronize()

@@ -434,3 +434,43 @@ def test_torch_materialize_post_mask_is_needed():
     short = torch.isinf(val[0])
     assert bool(short.any()) and bool((idx[0][short] == -1).all())
     assert bool((idx[0][~short] >= 0).all())
+
+
+# ---------------------------------------------------------------------------
+# fp16 operands of the attention oracle
+# ---------------------------------------------------------------------------
+def test_f16_decoder_matches_numpy_on_every_bit_pattern():
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))  # exact, signed zeros included
+
+
+def test_attn_oracle_f16_matches_numpy_restatement():
+    """The C oracle on fp16 operands equals the numpy restatement run on the
+    same values; the same values as bf16 bits give a different answer (the
+    flag selects the decoding)."""
+    rng = np.random.default_rng(21)
+    n, H, D, N, K = 5, 4, 32, 40, 12
+    q = (rng.standard_normal((n, H, D)) * 0.7).astype(np.float16)
+    kv = (rng.standard_normal((N, D)) * 0.7).astype(np.float16)
+    sink = rng.standard_normal(H).astype(np.float32)
+    idx = rng.integers(-1, N, size=(n, K))
+    o, lse = O.sparse_attn_rows(q.view(np.uint16), kv.view(np.uint16), sink, idx, D ** -0.5, f16=True)
+    ro, rl = O.np_sparse_attn(q.astype(np.float64), kv.astype(np.float64), sink, idx, D ** -0.5)
+    assert np.allclose(o, ro, rtol=1e-12, atol=1e-12) and np.allclose(lse, rl, rtol=1e-12, atol=1e-12)
+    wrong, _ = O.sparse_attn_rows(q.view(np.uint16), kv.view(np.uint16), sink, idx, D ** -0.5)
+    assert not np.allclose(wrong, ro, atol=1e-3)
+    # backward: fp16 finite differences of the fp16-valued forward are what the
+    # bf16 path's tests pin; here the flag must select the same decoding
+    do = (rng.standard_normal((n, H, D)) * 0.5).astype(np.float16)
+    of16 = o.astype(np.float16)
+    dq, dkv, ds = O.sparse_attn_bwd_rows(q.view(np.uint16), kv.view(np.uint16), of16.view(np.uint16),
+                                         do.view(np.uint16), sink, lse.astype(np.float32), idx, D ** -0.5, f16=True)
+    dq2, dkv2, ds2 = O.np_sparse_attn_bwd(q.astype(np.float64), kv.astype(np.float64), of16.astype(np.float64),
+                                          do.astype(np.float64), sink, lse.astype(np.float32).astype(np.float64), idx,
+                                          D ** -0.5)
+    assert np.allclose(dq, dq2, rtol=1e-10, atol=1e-12) and np.allclose(dkv, dkv2, rtol=1e-10, atol=1e-12)
+    assert np.allclose(ds, ds2, rtol=1e-10, atol=1e-12)

@@ -45,7 +45,8 @@ def _args(p, outs):
     head = (q.data_ptr(), L.strides(q), kv.data_ptr(), L.strides(kv), sink.data_ptr(), idx.data_ptr(),
             1 if idx.dtype == torch.int64 else 0, L.strides(idx), o.data_ptr(), L.strides(o), lse.data_ptr(),
             L.strides(lse), do.data_ptr(), L.strides(do), B, S, H, D, kv.shape[1], idx.shape[2], D ** -0.5,
-            dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv), dsink.data_ptr())
+            1 if q.dtype == torch.float16 else 0, dq.data_ptr(), L.strides(dq), dkv.data_ptr(), L.strides(dkv),
+            dsink.data_ptr())
     rl = (None, None) if row_len is None else (row_len.data_ptr(), L.strides(row_len))
     return head, rl
 
