@@ -63,8 +63,8 @@ size_t si_indexer_topk_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t 
  *                     Must be 0 when mask != NULL.
  *   out_idx    [B,S,top_k] int64, contiguous: best-first, -1 past the legal count
  *   out_scores [B,S,top_k] fp32,  contiguous: best-first, -inf past the legal count
- * Ties rank the smaller key index first.  Supported: H <= 64, D in {32,64,128},
- * 1 <= top_k <= 2048.
+ * Ties rank the smaller key index first.  Supported: D in {32,64,128} with
+ * H <= 128, D = 256 with H <= 64 and top_k <= 1536; 1 <= top_k <= 2048.
  */
 int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, const int64_t* k_strides,
                     const void* weights, int w_dtype, const int64_t* w_strides, const uint8_t* mask,

@@ -30,13 +30,21 @@ static int dispatch_shape(const IndexerArgs& a, int D, hipStream_t st) {
   SI_CASE(1, 32)
   SI_CASE(1, 64)
   SI_CASE(1, 128)
+  SI_CASE(1, 256)
   SI_CASE(2, 32)
   SI_CASE(2, 64)
   SI_CASE(2, 128)
+  SI_CASE(2, 256)
+  SI_CASE(3, 32)
+  SI_CASE(3, 64)
+  SI_CASE(3, 128)
+  SI_CASE(4, 32)
+  SI_CASE(4, 64)
+  SI_CASE(4, 128)
 #undef SI_CASE
   return set_error(SI_ERR_UNSUPPORTED,
                    "unsupported indexer shape: H_I=" + std::to_string(a.H) + " D_I=" + std::to_string(D) +
-                       " (supported: H_I<=64, D_I in {32,64,128})");
+                       " (supported: D_I in {32,64,128} with H_I<=128, D_I=256 with H_I<=64)");
 }
 
 static int fill_common(IndexerArgs& a, const void* q, const int64_t* qs, const void* k, const int64_t* ks,

@@ -1,4 +1,5 @@
-// Instantiates the lightning-indexer kernels for head dim D_I = 32.
+// Instantiates the lightning-indexer kernels for head dim D_I = 32
+// (32-head blocks 1, 2: H_I up to 64).
 #include "indexer_kernels.h"
 
 namespace si {

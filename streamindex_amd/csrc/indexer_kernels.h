@@ -248,11 +248,28 @@ template <int C>
 struct TopkShape {
   static constexpr int NW = 4;
   static constexpr int TILE_N = 64;
-  static constexpr int WAVES_PER_EU = C <= 1536 ? 2 : 1;
+  static constexpr int WAVES_PER_EU = C <= 1536 ? 2 : 1;  // for one or two 32-head blocks at D <= 128
   // K tiles in the LDS ring: tile i+1 is copied while tile i is consumed (a
   // third buffer measured no faster at S = 64K).
   static constexpr int RING = 2;
 };
+
+// Workgroups per CU of the bf16 top-k kernel.  Up to two 32-head blocks at
+// D <= 128 a row's Q fragments, head weights and pipelined accumulators fit
+// 256 VGPRs, so two workgroups share a CU (up to C = 1536); wider query rows
+// (H > 64 or D = 256) hold twice the registers and run one workgroup per CU.
+template <int HB, int D, int C>
+constexpr int topk_waves_per_eu() {
+  return (HB <= 2 && D <= 128) ? TopkShape<C>::WAVES_PER_EU : 1;
+}
+
+// Whether the K ring and the selection buffers of a (D, C) instance fit the
+// LDS share of one workgroup.
+template <int HB, int D, int C>
+constexpr bool topk_fits_lds() {
+  return TopkShape<C>::RING * TopkShape<C>::TILE_N * D * 2 + TopkShape<C>::NW * C * 8 <=
+         160 * 1024 / topk_waves_per_eu<HB, D, C>();
+}
 
 // s_waitcnt with vmcnt = n (0..15), lgkmcnt = 0, expcnt not waited (gfx9 encoding).
 template <int N>
@@ -266,7 +283,7 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // ---------------------------------------------------------------------------
 template <int HB, int D, int C, bool MASKED>
 __global__ __launch_bounds__(TopkShape<C>::NW * 64)
-__attribute__((amdgpu_waves_per_eu(TopkShape<C>::WAVES_PER_EU, TopkShape<C>::WAVES_PER_EU)))
+__attribute__((amdgpu_waves_per_eu(topk_waves_per_eu<HB, D, C>(), topk_waves_per_eu<HB, D, C>())))
 void indexer_topk_kernel(IndexerArgs a) {
   constexpr int NW = TopkShape<C>::NW;
   constexpr int NT = NW * 64;
@@ -284,7 +301,7 @@ void indexer_topk_kernel(IndexerArgs a) {
   // posted before each tile barrier, where LDS has room for them.
   constexpr int SEL_END = RING * TILE_BYTES + NW * C * 8;
   // LDS per workgroup so that WAVES_PER_EU workgroups share a CU's 160 KiB.
-  constexpr int LDS_BUDGET = 160 * 1024 / TopkShape<C>::WAVES_PER_EU;
+  constexpr int LDS_BUDGET = 160 * 1024 / topk_waves_per_eu<HB, D, C>();
   constexpr bool SHARE_COMP = SEL_END + 2 * NW * 4 <= LDS_BUDGET;
   static_assert(SEL_END <= LDS_BUDGET, "ring + selection buffers exceed the LDS share");
   __shared__ __attribute__((aligned(16))) char lds[SEL_END + (SHARE_COMP ? 2 * NW * 4 : 0)];
@@ -558,6 +575,9 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
 // ---------------------------------------------------------------------------
 template <int HB, int D, int C>
 int launch_topk(const IndexerArgs& a, hipStream_t st) {
+  if constexpr (!topk_fits_lds<HB, D, C>()) {
+    return set_error(SI_ERR_UNSUPPORTED, "top_k too large for this head dim (the selection buffers exceed LDS)");
+  } else {
   constexpr int NW = TopkShape<C>::NW;
   const int nqb = (a.S + NW - 1) / NW;
   const int64_t nblk = static_cast<int64_t>(nqb) * a.B;
@@ -570,11 +590,14 @@ int launch_topk(const IndexerArgs& a, hipStream_t st) {
                        0, st, a);
   }
   return check_launch("indexer_topk_kernel");
+  }
 }
 
 template <int HB, int D>
 int launch_score(const IndexerArgs& a, hipStream_t st) {
-  constexpr int NW = 8;
+  // 8 rows per workgroup (two waves per SIMD) up to two head blocks at
+  // D <= 128; wider rows need a SIMD's registers for one wave.
+  constexpr int NW = (HB <= 2 && D <= 128) ? 8 : 4;
   constexpr int TILE_N = 128;
   const int nqb = (a.S + NW - 1) / NW;
   const int64_t nblk = static_cast<int64_t>(nqb) * a.B;

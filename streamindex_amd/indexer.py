@@ -23,9 +23,12 @@ import torch
 
 from . import _lib
 
-SUPPORTED_D = (32, 64, 128)
-MAX_HEADS = 64
+SUPPORTED_D = (32, 64, 128, 256)
+MAX_HEADS = 128          # D_I <= 128
+MAX_HEADS_D256 = 64      # D_I = 256: the row's Q fragments take twice the registers
 MAX_TOPK = 2048
+MAX_TOPK_D256 = 1536     # D_I = 256: 32 KiB key tiles leave LDS for 2048-key selection buffers
+MAX_HEADS_Q = 64         # fp4 q / fp8 k indexer
 
 
 def _check_common(q: torch.Tensor, k_idx: torch.Tensor, weights: torch.Tensor):
@@ -42,8 +45,9 @@ def _check_common(q: torch.Tensor, k_idx: torch.Tensor, weights: torch.Tensor):
         raise ValueError(f"weights must be float32 or bfloat16, got {weights.dtype}")
     if D_I not in SUPPORTED_D:
         raise ValueError(f"D_I ({D_I}) must be one of {SUPPORTED_D}")
-    if H_I > MAX_HEADS:
-        raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS}")
+    max_h = MAX_HEADS_D256 if D_I == 256 else MAX_HEADS
+    if H_I > max_h:
+        raise ValueError(f"H_I ({H_I}) must be <= {max_h} for D_I = {D_I}")
     return B, S, H_I, D_I, T
 
 
@@ -86,8 +90,9 @@ def _topk_launch(q, k_idx, weights, top_k, causal_mask, causal_ratio):
     B, S, H_I, D_I, T = _check_common(q, k_idx, weights)
     if top_k <= 0:
         raise ValueError(f"top_k must be positive, got {top_k}")
-    if top_k > MAX_TOPK:
-        raise ValueError(f"top_k ({top_k}) must be <= {MAX_TOPK}")
+    max_k = MAX_TOPK_D256 if D_I == 256 else MAX_TOPK
+    if top_k > max_k:
+        raise ValueError(f"top_k ({top_k}) must be <= {max_k} for D_I = {D_I}")
     q, k_idx, weights = _prep(q, k_idx, weights)
     out_idx = torch.empty((B, S, top_k), dtype=torch.int64, device=q.device)
     out_scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q.device)
@@ -233,8 +238,8 @@ def indexer_topk_q(
         raise ValueError(f"weights must be float32 or bfloat16, got {weights.dtype}")
     if D_I != 128:
         raise ValueError(f"D_I ({D_I}) must be 128 for quantised inputs")
-    if H_I > MAX_HEADS:
-        raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS}")
+    if H_I > MAX_HEADS_Q:
+        raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS_Q} for quantised inputs")
     if top_k <= 0 or top_k > MAX_TOPK:
         raise ValueError(f"top_k must be in [1, {MAX_TOPK}], got {top_k}")
     if check_scales and q_scale.numel():

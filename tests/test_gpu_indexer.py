@@ -67,12 +67,30 @@ def test_t_smaller_than_topk(cuda_device):
     check_indexer(q, k, w, 512, idx, sc, causal_ratio=4, label="T<k")
 
 
-@pytest.mark.parametrize("H,D", [(16, 32), (16, 64), (32, 128), (48, 64), (64, 32), (64, 64), (64, 128)])
+@pytest.mark.parametrize("H,D", [(16, 32), (16, 64), (32, 128), (48, 64), (64, 32), (64, 64), (64, 128),
+                                 (80, 128), (96, 64), (128, 32), (128, 64), (128, 128), (16, 256), (64, 256)])
 def test_head_shapes(cuda_device, H, D):
     q, k, w = _inputs(1, 128, H, D, 300, 40 + H + D)
     idx, sc = chunked_indexer_topk(q, k, w, 40)
     torch.cuda.synchronize()
     check_indexer(q, k, w, 40, idx, sc, label=f"H={H},D={D}")
+
+
+@pytest.mark.parametrize("H,D,top_k,ratio", [(128, 128, 512, 4), (128, 128, 1024, None), (128, 128, 2048, None),
+                                             (64, 256, 512, 4), (64, 256, 1536, None), (100, 64, 700, 2)])
+def test_wide_rows(cuda_device, H, D, top_k, ratio):
+    """H_I up to 128 (one workgroup per CU) and D_I = 256 at several
+    selection capacities, causal and not, through the oracle gate; the score
+    matrix of the same shapes against the oracle."""
+    S, T = 96, 2500 if ratio is None else 96 // ratio
+    q, k, w = _inputs(1, S, H, D, T, 7 + H + D + top_k)
+    idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio)
+    torch.cuda.synchronize()
+    check_indexer(q, k, w, top_k, idx, sc, causal_ratio=ratio, label=f"H={H},D={D},k={top_k}")
+    s = indexer_score(q[:, :16], k, w[:, :16])
+    torch.cuda.synchronize()
+    ref = O.indexer_scores(bf16_bits(q[0, :16]), bf16_bits(k[0]), w[0, :16].cpu().numpy())
+    assert np.allclose(s[0].cpu().numpy(), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).mean())
 
 
 @pytest.mark.parametrize("top_k", [1, 7, 64, 65, 100, 128, 129, 256, 257, 512, 513, 640, 641, 700, 1024, 1152,
@@ -231,3 +249,8 @@ def test_invalid_arguments_raise(cuda_device):
     with pytest.raises(ValueError):
         q5, k5, w5 = _inputs(1, 16, 16, 48, 16, 3)
         chunked_indexer_topk(q5, k5, w5, 4)
+    # the limits of the wide shapes: H_I > 128, H_I > 64 at D_I = 256, top_k > 1536 at D_I = 256
+    for (H, D, kk) in ((160, 64, 4), (96, 256, 4), (32, 256, 2048)):
+        qq, kk_, ww = _inputs(1, 8, H, D, 16, 4)
+        with pytest.raises(ValueError):
+            chunked_indexer_topk(qq, kk_, ww, kk)
