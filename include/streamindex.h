@@ -313,6 +313,18 @@ int si_token_compress(const void* c_a, const void* z_a, const float* b_a, const 
 int si_gated_pool(const void* kv, const void* score, void* out, int dtype, int64_t outer, int64_t L, int64_t inner,
                   void* stream);
 
+/*
+ * Synthetic inputs for benchmarks and tests (no counterpart in the reference,
+ * whose harnesses draw with torch.randn on a CUDA generator,
+ * eval/test_v4_indexer_parity.py:89-103): out[i] = N(0,1)[seed, stream, i]
+ * * scale, i < n, as fp32 (dtype 0) or bf16 rounded to nearest even (dtype 1).
+ * Element i depends on (seed, stream, i) only (Philox4x32-10 counter (i/4,
+ * stream, 0), Box-Muller with IEEE-exact ln / sin / cos polynomials), so the
+ * same tensor results on every device and launch shape and any slice can be
+ * recomputed on the CPU.
+ */
+int si_fill_normal(void* out, int dtype, int64_t n, uint64_t seed, uint32_t stream, float scale, void* stream_ptr);
+
 #ifdef __cplusplus
 }
 #endif

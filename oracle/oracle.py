@@ -85,6 +85,14 @@ def lib() -> ctypes.CDLL:
         L.oracle_sparse_attn_bwd_t.restype = None
         L.oracle_f16_to_f32.argtypes = [P, I, P]
         L.oracle_f16_to_f32.restype = None
+        L.oracle_fill_normal.argtypes = [I, I, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, P, P]
+        L.oracle_fill_normal.restype = None
+        L.oracle_normal_digest.argtypes = [ctypes.c_int, I, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, P, P]
+        L.oracle_normal_digest.restype = None
+        L.oracle_philox4x32_10.argtypes = [P, P, P]
+        L.oracle_philox4x32_10.restype = None
+        L.oracle_fill_normal_at.argtypes = [P, I, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, P, P]
+        L.oracle_fill_normal_at.restype = None
         _lib = L
     return _lib
 
@@ -188,6 +196,49 @@ def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
     out = np.empty(b.shape, dtype=np.float32)
     lib().oracle_f16_to_f32(_ptr(b), b.size, _ptr(out))
     return out
+
+
+def synth_normal(start: int, n: int, seed: int, stream: int, scale: float = 1.0, bf16: bool = False) -> np.ndarray:
+    """Elements [start, start + n) of the counter-based synthetic tensor
+    (seed, stream) times ``scale``: float32, or bf16 bit patterns (uint16).
+    Restates ``streamindex_amd/csrc/synth.hip`` (``si_fill_normal``)."""
+    if bf16:
+        out = np.empty(n, dtype=np.uint16)
+        lib().oracle_fill_normal(start, n, seed, stream, scale, None, _ptr(out))
+    else:
+        out = np.empty(n, dtype=np.float32)
+        lib().oracle_fill_normal(start, n, seed, stream, scale, _ptr(out), None)
+    return out
+
+
+def synth_normal_at(idx: np.ndarray, seed: int, stream: int, scale: float = 1.0, bf16: bool = False) -> np.ndarray:
+    """The synthetic tensor (seed, stream) at the flat indices ``idx``."""
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    if bf16:
+        out = np.empty(idx.shape, dtype=np.uint16)
+        lib().oracle_fill_normal_at(_ptr(idx), idx.size, seed, stream, scale, None, _ptr(out))
+    else:
+        out = np.empty(idx.shape, dtype=np.float32)
+        lib().oracle_fill_normal_at(_ptr(idx), idx.size, seed, stream, scale, _ptr(out), None)
+    return out
+
+
+def philox4x32_10(ctr, key) -> tuple:
+    """One Philox4x32-10 block: 4 counter words, 2 key words -> 4 words."""
+    c = np.asarray(ctr, dtype=np.uint32)
+    k = np.asarray(key, dtype=np.uint32)
+    out = np.empty(4, dtype=np.uint32)
+    lib().oracle_philox4x32_10(_ptr(c), _ptr(k), _ptr(out))
+    return tuple(int(x) for x in out)
+
+
+def synth_digest(n: int, seed: int, stream: int, scale: float = 1.0, bf16: bool = False):
+    """(d1, d2) over the little-endian 16-bit words w_j of the whole tensor:
+    d1 = sum w_j, d2 = sum w_j (j mod 65521 + 1), both mod 2^64."""
+    d1 = np.zeros(1, dtype=np.uint64)
+    d2 = np.zeros(1, dtype=np.uint64)
+    lib().oracle_normal_digest(1 if bf16 else 0, n, seed, stream, scale, _ptr(d1), _ptr(d2))
+    return int(d1[0]), int(d2[0])
 
 
 def sparse_attn_rows(q_bits: np.ndarray, kv_bits: np.ndarray, sink: np.ndarray, idx: np.ndarray, scale: float,

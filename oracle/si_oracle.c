@@ -371,3 +371,191 @@ void oracle_sparse_attn_bwd(const uint16_t* q, const uint16_t* kv, const uint16_
   oracle_sparse_attn_bwd_t(q, kv, o, dout, sink, lse, idx, nrows, H, D, N, K, scale, key_slot, nslot, 0, dq, dkv,
                            dsink);
 }
+
+/*
+ * Counter-based N(0,1) draws: the CPU restatement of the generator in
+ * streamindex_amd/csrc/synth.hip (Philox4x32-10 as published by Salmon et al.,
+ * SC 2011; Box-Muller with ln / sin / cos, reciprocal and square root built
+ * from additions, multiplies and fused multiply-adds only), so a slice of any
+ * synthetic tensor can be recomputed here bit for bit.  Element i of (seed, stream): counter (i/4, stream, 0),
+ * word pair (2 (i%4 / 2), +1), cosine for even i%4, sine for odd.
+ */
+static void syn_philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0;
+    c[1] = lo1;
+    c[2] = n2;
+    c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+static float syn_u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+static uint32_t syn_f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  return u;
+}
+
+static float syn_recip(float d) {
+  float y = fmaf(-0.225f, d, 0.96f);
+  for (int i = 0; i < 3; ++i) y = fmaf(y, fmaf(-d, y, 1.0f), y);
+  return y;
+}
+
+static float syn_sqrt(float t) {
+  if (!(t > 0.0f)) return 0.0f;
+  float y = syn_u2f(0x5F3759DFu - (syn_f2u(t) >> 1));
+  const float h = 0.5f * t;
+  for (int i = 0; i < 3; ++i) y = y * fmaf(-(h * y), y, 1.5f);
+  return t * y;
+}
+
+static float syn_log(float u) {
+  const uint32_t b = syn_f2u(u);
+  int e = (int)(b >> 23) - 127;
+  float m = syn_u2f((b & 0x7FFFFFu) | 0x3F800000u);
+  if (m > 1.41421356f) {
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float s = (m - 1.0f) * syn_recip(m + 1.0f);
+  const float s2 = s * s;
+  float p = fmaf(s2, 0.18181818f, 0.22222222f);
+  p = fmaf(s2, p, 0.28571429f);
+  p = fmaf(s2, p, 0.4f);
+  p = fmaf(s2, p, 0.66666667f);
+  const float lnm = fmaf(s * s2, p, 2.0f * s);
+  const float ef = (float)e;
+  return fmaf(ef, 0.693145752f, fmaf(ef, 1.42860677e-06f, lnm));
+}
+
+static void syn_sincos(float phi, float* c, float* s) {
+  const float x2 = phi * phi;
+  float pc = fmaf(x2, 2.08767570e-09f, -2.75573192e-07f);
+  pc = fmaf(x2, pc, 2.48015873e-05f);
+  pc = fmaf(x2, pc, -1.38888889e-03f);
+  pc = fmaf(x2, pc, 4.16666667e-02f);
+  pc = fmaf(x2, pc, -0.5f);
+  *c = fmaf(x2, pc, 1.0f);
+  float ps = fmaf(x2, -2.50521084e-08f, 2.75573192e-06f);
+  ps = fmaf(x2, ps, -1.98412698e-04f);
+  ps = fmaf(x2, ps, 8.33333333e-03f);
+  ps = fmaf(x2, ps, -0.166666667f);
+  *s = fmaf(phi * x2, ps, phi);
+}
+
+static void syn_box_muller(uint32_t x, uint32_t y, float* n0, float* n1) {
+  const float u1 = (float)((x >> 8) + 1u) * 5.9604644775390625e-08f;
+  const float r = syn_sqrt(-2.0f * syn_log(u1));
+  const uint32_t y24 = y >> 8;
+  const uint32_t quad = y24 >> 22;
+  const float phi = (float)(y24 & 0x3FFFFFu) * 2.384185791015625e-07f * 1.57079637f;
+  float c, s, cs, sn;
+  syn_sincos(phi, &c, &s);
+  if (quad == 0) {
+    cs = c; sn = s;
+  } else if (quad == 1) {
+    cs = -s; sn = c;
+  } else if (quad == 2) {
+    cs = -c; sn = -s;
+  } else {
+    cs = s; sn = -c;
+  }
+  *n0 = r * cs;
+  *n1 = r * sn;
+}
+
+static void syn_quad(uint64_t q, uint32_t k0, uint32_t k1, uint32_t stream, float v[4]) {
+  uint32_t c[4] = {(uint32_t)q, (uint32_t)(q >> 32), stream, 0u};
+  syn_philox(c, k0, k1);
+  syn_box_muller(c[0], c[1], &v[0], &v[1]);
+  syn_box_muller(c[2], c[3], &v[2], &v[3]);
+}
+
+static uint16_t syn_bf16(float f) {
+  const uint32_t u = syn_f2u(f);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+/* Elements [start, start + n) scaled: fp32 (out32) or bf16 bits (out16); the other may be NULL. */
+void oracle_fill_normal(int64_t start, int64_t n, uint64_t seed, uint32_t stream, float scale, float* out32,
+                        uint16_t* out16) {
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t g = start + i;
+    float v[4];
+    syn_quad((uint64_t)g >> 2, k0, k1, stream, v);
+    const float x = v[g & 3] * scale;
+    if (out32) out32[i] = x;
+    if (out16) out16[i] = syn_bf16(x);
+  }
+}
+
+/*
+ * Digest of a whole synthetic tensor of n elements (dtype 0 fp32, 1 bf16),
+ * over its little-endian 16-bit words w_j: d1 = sum w_j, d2 = sum w_j (j mod
+ * 65521 + 1), both mod 2^64.
+ */
+void oracle_normal_digest(int dtype, int64_t n, uint64_t seed, uint32_t stream, float scale, uint64_t* d1,
+                          uint64_t* d2) {
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  const int64_t nq = (n + 3) / 4;
+  uint64_t a = 0, b = 0;
+#pragma omp parallel for schedule(static) reduction(+ : a, b)
+  for (int64_t q = 0; q < nq; ++q) {
+    float v[4];
+    syn_quad((uint64_t)q, k0, k1, stream, v);
+    for (int t = 0; t < 4; ++t) {
+      const int64_t i = q * 4 + t;
+      if (i >= n) break;
+      const float x = v[t] * scale;
+      if (dtype == 1) {
+        const uint64_t w = syn_bf16(x);
+        a += w;
+        b += w * (uint64_t)(i % 65521 + 1);
+      } else {
+        const uint32_t u = syn_f2u(x);
+        const uint64_t lo = u & 0xFFFFu, hi = u >> 16;
+        const int64_t j = 2 * i;
+        a += lo + hi;
+        b += lo * (uint64_t)(j % 65521 + 1) + hi * (uint64_t)((j + 1) % 65521 + 1);
+      }
+    }
+  }
+  *d1 = a;
+  *d2 = b;
+}
+
+/* One Philox4x32-10 block (the bijection the generator draws from). */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c[4] = {ctr[0], ctr[1], ctr[2], ctr[3]};
+  syn_philox(c, key[0], key[1]);
+  memcpy(out, c, sizeof c);
+}
+
+/* Synthetic elements at arbitrary flat indices idx[0..n), scaled; fp32 or bf16 bits. */
+void oracle_fill_normal_at(const int64_t* idx, int64_t n, uint64_t seed, uint32_t stream, float scale, float* out32,
+                           uint16_t* out16) {
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t g = idx[i];
+    float v[4];
+    syn_quad((uint64_t)g >> 2, k0, k1, stream, v);
+    const float x = v[g & 3] * scale;
+    if (out32) out32[i] = x;
+    if (out16) out16[i] = syn_bf16(x);
+  }
+}

@@ -65,6 +65,7 @@ SIGNATURES = {
     "si_sparse_attn_bwd_ragged": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                                          _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                          _P, _I64P, _P, _I64P, _P, _P, _I64, _P, _I64P, _P]),
+    "si_fill_normal": (_I32, [_P, _I32, _I64, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, _P]),
     "si_sparse_attn_bwd_noalloc_scratch_bytes": (_I64, []),
     "si_sparse_attn_bwd_noalloc": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                                           _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
