@@ -72,6 +72,23 @@ int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, 
                     int64_t top_k, int64_t causal_ratio, int64_t* out_idx, float* out_scores, void* stream);
 
 /*
+ * Which top-k kernel si_indexer_topk and si_csa_indexer_topk launch
+ * (process-wide; returns the previous setting).  No counterpart in the
+ * reference: a tuning and test knob.  SI_TOPK_KERNEL_AUTO (default) runs
+ * the four-32-head-block kernel for D = 128 with H in (96, 128], or H in
+ * (32, 64] and rows of at least 64K legal keys, and the
+ * two-workgroups-per-CU kernel otherwise; _NARROW and _WIDE force one of
+ * them where the shape allows (WIDE falls back to NARROW for the shapes
+ * only NARROW serves, e.g. top_k > 1152 at H <= 64).  Both return
+ * identical results.  Returns the previous mode, or -1 for a mode
+ * outside 0..2.
+ */
+#define SI_TOPK_KERNEL_AUTO 0
+#define SI_TOPK_KERNEL_NARROW 1
+#define SI_TOPK_KERNEL_WIDE 2
+int si_indexer_set_topk_kernel(int mode);
+
+/*
  * Materialised indexer score matrix scores[b,s,t] = sum_h w[b,s,h]*relu(q[b,s,h,:].k[b,t,:]),
  * fp32 with strides score_strides[3].  No mask.
  * Replaces flash_sparse/triton/indexer_score.py:41-179 (_indexer_score_kernel, indexer_score).

@@ -43,8 +43,13 @@ COMMON_FLAGS = [
 # accumulators in VGPRs (not AGPRs): its rare online-softmax rescale multiplies
 # them with VALU, and AGPR-resident accumulators made the compiler copy all of
 # them into VGPRs on every loop iteration.
+# The indexer units likewise: the four-M-block top-k kernel keeps its Q
+# fragments in AGPRs (MFMA A-operands only) and its accumulators in VGPRs,
+# where the fp32 epilogue reads them.
 EXTRA_FLAGS = {
     "sparse_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    **{f"indexer_inst_{u}.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+       for u in ("d32", "d32_wide", "d64", "d64_wide", "d128", "d128_wide", "d256")},
 }
 
 

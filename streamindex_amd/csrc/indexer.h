@@ -41,6 +41,36 @@ struct IndexerArgs {
 template <int HB, int D, int C>
 int launch_topk(const IndexerArgs& a, hipStream_t st);
 
+// Shapes served by the four-M-block top-k kernel (indexer_topk_wide.h):
+// HB = 2 (two rows per wave, 8 rows per workgroup) or HB = 4 (one row per
+// wave), D = 128, and LDS for its 3-slot K ring (64-key tiles) plus the
+// workgroup's selection buffers and compaction requests.
+template <int HB, int D, int C>
+constexpr bool topk_wide_fits() {
+  return (HB == 2 || HB == 4) && D == 128 && 3 * 64 * D * 2 + 4 * (4 / HB) * C * 8 + 3 * 4 * 4 <= 160 * 1024;
+}
+
+template <int HB, int D, int C>
+int launch_topk_wide(const IndexerArgs& a, hipStream_t st);
+
+// Top-k kernel choice (SI_TOPK_KERNEL_AUTO / _NARROW / _WIDE, set through
+// si_indexer_set_topk_kernel).
+extern int g_topk_kernel_mode;
+
+// Whether the four-M-block kernel is the faster one (measured): always for
+// one 128-head row per wave (the other kernel then runs one wave per SIMD
+// too), and for two 64-head rows per wave when rows reach 64K legal keys
+// (its single wave per SIMD pays per-row costs -- final sort, compactions,
+// workgroup tail -- that the two-workgroup-per-CU indexer_topk_kernel
+// hides, and wins in the MFMA loop that long rows spend their time in).
+inline bool topk_wide_preferred(const IndexerArgs& a) {
+  if (g_topk_kernel_mode == 1) return false;
+  if (g_topk_kernel_mode == 2) return true;
+  if (a.H > 96) return true;
+  const int64_t tmax = a.ratio > 0 ? (a.S / a.ratio < a.T ? a.S / a.ratio : a.T) : a.T;
+  return tmax >= 65536;
+}
+
 template <int HB, int D>
 int launch_score(const IndexerArgs& a, hipStream_t st);
 

@@ -7,10 +7,22 @@
 
 namespace si {
 
+int g_topk_kernel_mode = 0;
+
 template <int HB, int D>
 static int dispatch_kcap(const IndexerArgs& a, hipStream_t st) {
   // A compaction keeps between top_k and C - 192 keys; the capacity is
-  // chosen so that this window leaves room for several 64-key offers.
+  // chosen so that this window leaves room for several 64-key offers.  The
+  // four-M-block kernel (HB 2 and 4, D = 128, long rows) runs one workgroup
+  // per CU and stalls the CU while a row compacts, so it takes the largest
+  // capacity its LDS holds: compactions become rarer.
+  if constexpr (topk_wide_fits<HB, D, 1024>()) {
+    if (topk_wide_preferred(a)) {
+      if (a.top_k <= 192) return launch_topk_wide<HB, D, 1024>(a, st);
+      if (a.top_k <= 1152 && topk_wide_fits<HB, D, 2048>()) return launch_topk_wide<HB, D, 2048>(a, st);
+      if (a.top_k <= 1152) return launch_topk_wide<HB, D, 1536>(a, st);
+    }
+  }
   if (a.top_k <= 32) return launch_topk<HB, D, 256>(a, st);
   if (a.top_k <= 192) return launch_topk<HB, D, 512>(a, st);
   if (a.top_k <= 640) return launch_topk<HB, D, 1024>(a, st);
@@ -77,6 +89,13 @@ static int fill_common(IndexerArgs& a, const void* q, const int64_t* qs, const v
 }  // namespace si
 
 using namespace si;
+
+extern "C" int si_indexer_set_topk_kernel(int mode) {
+  if (mode < 0 || mode > 2) return set_error(SI_ERR_INVALID, "top-k kernel mode must be 0 (auto), 1 or 2"), -1;
+  const int prev = g_topk_kernel_mode;
+  g_topk_kernel_mode = mode;
+  return prev;
+}
 
 extern "C" int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx,
                                const int64_t* k_strides, const void* weights, int w_dtype,

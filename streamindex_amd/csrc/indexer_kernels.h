@@ -88,6 +88,15 @@ struct KTileLoader {
     }
   }
 
+  // Copy i (0 <= i < LPT) of a tile that lies inside [0, T), whose first
+  // key row starts at `src`.
+  __device__ __forceinline__ void issue_at(const char* src, char* tile, int i) const {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot0 = i * NTHREADS + wave * 64;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint16_t*>(src + voff[i]), (lds_void*)(tile + slot0 * 16),
+                                     16, 0, 0);
+  }
+
   __device__ __forceinline__ void issue(const uint16_t* kb, int64_t kst, int t0, int T, char* tile) const {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (t0 + TILE_N <= T) {
@@ -219,7 +228,7 @@ __device__ __forceinline__ void static_for_impl(F& f) {
   }
 }
 template <int N, typename F>
-__device__ __forceinline__ void static_for(F& f) {
+__device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<0, N>(f);
 }
 
@@ -569,51 +578,5 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
     tile_barrier();
   }
 }
-
-// ---------------------------------------------------------------------------
-// Launchers.
-// ---------------------------------------------------------------------------
-template <int HB, int D, int C>
-int launch_topk(const IndexerArgs& a, hipStream_t st) {
-  if constexpr (!topk_fits_lds<HB, D, C>()) {
-    return set_error(SI_ERR_UNSUPPORTED, "top_k too large for this head dim (the selection buffers exceed LDS)");
-  } else {
-  constexpr int NW = TopkShape<C>::NW;
-  const int nqb = (a.S + NW - 1) / NW;
-  const int64_t nblk = static_cast<int64_t>(nqb) * a.B;
-  if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  if (a.mask) {
-    hipLaunchKernelGGL((indexer_topk_kernel<HB, D, C, true>), dim3(static_cast<unsigned>(nblk)), dim3(NW * 64),
-                       0, st, a);
-  } else {
-    hipLaunchKernelGGL((indexer_topk_kernel<HB, D, C, false>), dim3(static_cast<unsigned>(nblk)), dim3(NW * 64),
-                       0, st, a);
-  }
-  return check_launch("indexer_topk_kernel");
-  }
-}
-
-template <int HB, int D>
-int launch_score(const IndexerArgs& a, hipStream_t st) {
-  // 8 rows per workgroup (two waves per SIMD) up to two head blocks at
-  // D <= 128; wider rows need a SIMD's registers for one wave.
-  constexpr int NW = (HB <= 2 && D <= 128) ? 8 : 4;
-  constexpr int TILE_N = 128;
-  const int nqb = (a.S + NW - 1) / NW;
-  const int64_t nblk = static_cast<int64_t>(nqb) * a.B;
-  if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((indexer_score_kernel<HB, D, NW, TILE_N>), dim3(static_cast<unsigned>(nblk)),
-                     dim3(NW * 64), 0, st, a);
-  return check_launch("indexer_score_kernel");
-}
-
-#define SI_INSTANTIATE_INDEXER(HB, D)                                   \
-  template int launch_score<HB, D>(const IndexerArgs&, hipStream_t);    \
-  template int launch_topk<HB, D, 256>(const IndexerArgs&, hipStream_t);  \
-  template int launch_topk<HB, D, 512>(const IndexerArgs&, hipStream_t);  \
-  template int launch_topk<HB, D, 1024>(const IndexerArgs&, hipStream_t); \
-  template int launch_topk<HB, D, 1536>(const IndexerArgs&, hipStream_t); \
-  template int launch_topk<HB, D, 2048>(const IndexerArgs&, hipStream_t); \
-  template int launch_topk<HB, D, 4096>(const IndexerArgs&, hipStream_t);
 
 }  // namespace si

@@ -56,7 +56,12 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.si_abi_version() == 6
+    assert lib.si_abi_version() == 7
+    # the top-k kernel knob: previous mode returned, out-of-range rejected
+    assert lib.si_indexer_set_topk_kernel(2) == 0
+    assert lib.si_indexer_set_topk_kernel(1) == 2
+    assert lib.si_indexer_set_topk_kernel(7) == -1
+    assert lib.si_indexer_set_topk_kernel(0) == 1
     assert lib.si_indexer_topk_workspace_bytes(1, 1 << 20, 1 << 18, 64, 128, 512) == 0
 
 
