@@ -104,6 +104,7 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
   static_assert(OFFER_G0 >= G && OFFER_G1 < G + MB, "offers run in the next tile's first half");
   static_assert(RPW == 1 || OFFER_G1 - OFFER_G0 >= 1, "one offer per group");
   static_assert(KS % 2 == 0, "a block's B-fragment reads are split over two groups");
+  static_assert(KS % 4 == 0, "the four offer steps are spread evenly over a group's chunks");
   static_assert(SEL_OFF <= 65536, "global_load_lds destinations stay below 64 KiB");
   static_assert(topk_wide_fits<HB, D, C>(), "ring + selection buffers exceed LDS");
   __shared__ __attribute__((aligned(16))) char lds[REQ_OFF + RING * NW * 4];
@@ -248,6 +249,8 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
     }
   };
 
+  int4 rq_prev = int4{0, 0, 0, 0};  // compaction requests posted at the previous mid-tile point
+
   // One tile.  SLOT (= it % RING) is a compile-time constant so every LDS
   // address is a per-lane base plus an immediate.  Each group is written as
   // KS chunks (one MFMA, its share of B-fragment reads, epilogue VALU and
@@ -318,12 +321,11 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
         }
         pin_vgpr(s0);
         pin_vgpr(s1);
-        // The offer's steps run in chunks 0 .. OFFER_PARTS-1 (in the last chunk
-        // when KS is smaller).  The next tile's copy is issued one load per
-        // chunk in groups MB, MB+1, ... (chunk 1 onwards).
+        // The offer's steps run every KS / OFFER_PARTS chunks from chunk 0, so
+        // that their VALU work hides behind as many MFMAs as possible.
         static_for<OFFER_PARTS>([&](auto PC) {
           constexpr int part = decltype(PC)::value;
-          if constexpr (orow >= 0 && (part < KS ? part == ks : ks == KS - 1))
+          if constexpr (orow >= 0 && part * (KS / OFFER_PARTS) == ks)
             offer_part(std::integral_constant<int, (orow < 0 ? 0 : orow)>{}, PC, tbase - TILE_N, it > 0,
                        mask_prev[orow < 0 ? 0 : orow]);
         });
@@ -338,27 +340,24 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
         // Mid-tile barrier: the copy of tile it+1 (issued one tile ago) has
         // landed and every wave is past its reads of tile it-1's slot, which
         // then takes the copy of tile it+2.  No copy is in flight between
-        // the barrier and that issue, which is where the compactions run: a
-        // row compacts when it could not take two more offers, or when it is
-        // close to that and some row of the workgroup needs one (so that the
-        // workgroup waits once for all of them).  Between two mid-tile
-        // points every row receives exactly one offer.
-        int need = 0;
-        static_for<RPW>([&](auto RC) { need |= sel[decltype(RC)::value].needs_compaction() ? 1 : 0; });
-        comp_req[slot * NW + wave] = need;
+        // the barrier and that issue, which is where the compactions run.
+        // Between two mid-tile points every row receives exactly one 64-key
+        // offer, so a row must compact when it holds more than C - 64 keys.
+        // A row that will need to at the next mid-tile point (more than
+        // C - 128 now) posts a request; the requests are read one tile later
+        // (no wait on the read), and then every row that is close to needing
+        // a compaction joins in, so the workgroup waits once for all of them.
+        int pred = 0;
+        static_for<RPW>([&](auto RC) { pred |= sel[decltype(RC)::value].needs_compaction() ? 1 : 0; });
+        comp_req[slot * NW + wave] = pred;
         wait_vm_lgkm0<0>();
         __syncthreads();
-        // (the requests are read only by waves with a row close to needing one)
-        bool wants = false;
-        static_for<RPW>([&](auto RC) { wants = wants || sel[decltype(RC)::value].wants_compaction(); });
-        if (wants) {
-          const int4 rq = *reinterpret_cast<const int4*>(comp_req + slot * NW);
-          const bool any = (rq.x | rq.y | rq.z | rq.w) != 0;
-          static_for<RPW>([&](auto RC) {
-            constexpr int r = decltype(RC)::value;
-            if (sel[r].needs_compaction() || (any && sel[r].wants_compaction())) compact_row(RC);
-          });
-        }
+        const bool any = (rq_prev.x | rq_prev.y | rq_prev.z | rq_prev.w) != 0;
+        rq_prev = *reinterpret_cast<const int4*>(comp_req + slot * NW);
+        static_for<RPW>([&](auto RC) {
+          constexpr int r = decltype(RC)::value;
+          if (sel[r].n > C - kWave || (any && sel[r].wants_compaction())) compact_row(RC);
+        });
         if (it + 2 < ntiles && (it + 3) * TILE_N <= a.T) {
           dma_src = reinterpret_cast<const char*>(kb + static_cast<int64_t>(it + 2) * TILE_N * a.kst);
           dma_dst = lds + fslot * TILE_BYTES;
@@ -387,7 +386,7 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
     });
     static_for<RPW>([&](auto RC) {
       constexpr int r = decltype(RC)::value;
-      if (sel[r].needs_compaction()) compact_row(RC);
+      if (sel[r].n > C - kWave) compact_row(RC);
     });
     const int tlast = (ntiles - 1) * TILE_N;
     static_for<RPW>([&](auto RC) {
