@@ -2,9 +2,10 @@
 matches the oracle.
 
 si_indexer_topk runs indexer_topk_kernel (two workgroups per CU, one query
-row per wave) or, for D_I = 128, H_I in (32, 64] or (96, 128] and rows of at
-least 64K legal keys, indexer_topk_wide_kernel (one wave per SIMD holding
-four 32-head blocks: two query rows, or one row of up to 128 heads).  The
+row per wave) or, for D_I = 128 with H_I in (96, 128], or H_I in (32, 64]
+and rows of at least 64K legal keys, indexer_topk_wide_kernel (one wave per
+SIMD holding four 32-head blocks: two query rows, or one row of up to 128
+heads).  The
 runtime switch si_indexer_set_topk_kernel forces either one, so the wide
 kernel is exercised here at sizes the oracle checks in seconds: every case
 compares the two kernels' indices and scores for exact equality (same fp32
@@ -13,8 +14,8 @@ oracle gate of tests/indexer_check.py.  Shapes cover the wide kernel's
 parts: partial head blocks, both selection capacities it uses (1024 for
 top_k <= 192, 1536 / 2048 above), tiles crossing T, T < 64 and T < top_k,
 the explicit mask, batch 2, S not a multiple of its 8-row workgroup, bf16
-weights, exact score ties, rows long enough for repeated compactions, and
-the CSA output rows.
+weights, exact score ties, rows long enough for repeated compactions, the
+CSA output rows, and config[2] in full.
 """
 
 from __future__ import annotations
@@ -140,3 +141,15 @@ def test_auto_picks_by_row_length(modes):
     a, b = _both(lambda: chunked_indexer_topk(q, k, w, 512, causal_ratio=4))
     _same(auto, a, "auto vs narrow")
     _same(auto, b, "auto vs wide")
+
+
+def test_config2_full_size_kernels_agree(modes):
+    # BASELINE config[2] (S=262,144, T=65,536, k=512): the automatic choice runs the
+    # four-M-block kernel here; the two kernels agree on every one of the 134M outputs.
+    q, k, w = synth.indexer_inputs(1, 262144, 64, 128, ratio=4, seed=2026)
+    a, b = _both(lambda: chunked_indexer_topk(q, k, w, 512, causal_ratio=4))
+    _same(a, b, "config[2]")
+    _set_mode(AUTO)
+    auto = chunked_indexer_topk(q, k, w, 512, causal_ratio=4)
+    torch.cuda.synchronize()
+    _same(auto, b, "config[2] auto")
