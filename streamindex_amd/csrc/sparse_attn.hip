@@ -142,7 +142,6 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       for (int ks = 0; ks < KS; ++ks)
         qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
     }
-    const float sink_v = hvalid ? a.sink[hq] : 0.f;
 
     // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
     // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
@@ -189,9 +188,10 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
       }
     };
-    auto issue_tile = [&](int t) {
-      read_roff(t, roff);
-      attn_static_for<0, SH::LPT>([&](auto IC) { dma(t, IC); });
+    // The copies of tile `src` (its row offsets) into the ring slot of tile `dst`.
+    auto issue_tile_from = [&](int src, int dst) {
+      read_roff(src, roff);
+      attn_static_for<0, SH::LPT>([&](auto IC) { dma(dst, IC); });
     };
 
 
@@ -299,15 +299,20 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
     const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (ntiles > 0) {
-      __syncthreads();  // indices of tiles 0..3 published
-      issue_tile(0);
-      if (ntiles > 1) issue_tile(1);
-      if (ntiles > 2) issue_tile(2);
-      // tile 0 landed; the copies of tiles 1 and 2 may still be in flight
-      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
-      else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-      __syncthreads();  // tile 0 landed
+      // (prologue barriers without a release fence, like the tile barrier: a
+      // fence would make the compiler wait here for the Q loads and for every
+      // tile copy in flight, not just the ones the comments name)
+      attn_tile_barrier();  // indices of tiles 0..3 published
+      // Copies of tiles 0, 1 and 2.  A row with fewer tiles copies its last
+      // tile again into the slots it does not use, so every row waits the same
+      // way and the compiler sees that the Q loads (issued first) have landed
+      // once tile 0 has.
+      issue_tile_from(0, 0);
+      issue_tile_from(ntiles > 1 ? 1 : ntiles - 1, 1);
+      issue_tile_from(ntiles > 2 ? 2 : ntiles - 1, 2);
+      // tile 0 (and every Q load) landed; the copies of tiles 1 and 2 may still be in flight
+      __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
+      attn_tile_barrier();  // tile 0 landed
       f32x4 bias_cur[2];
       {
         f32x4 bias[2], st[2] = {zero4, zero4};
@@ -319,10 +324,9 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         softmax_store(0, softmax(st, bias), live);
       }
       // tile 1 landed; the copies of tile 2 may still be in flight
-      if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-      __syncthreads();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
-      __syncthreads();  // indices of tile 4 published
+      __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+      attn_tile_barrier();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
+      attn_tile_barrier();  // indices of tile 4 published
       uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
       for (int it = 0; it < ntiles; ++it) {
         const bool issue = it + 3 < ntiles;
@@ -359,6 +363,9 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
     }
     constexpr float kLog2e = 1.4426950408889634f;
+    // (the sink is read only now: a load at the top would make the first
+    // copies wait for every Q load)
+    const float sink_v = hvalid ? a.sink[hq] : 0.f;
     const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
     const float m_fin = __builtin_fmaxf(m_ref, sink2);
     const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
