@@ -9,9 +9,11 @@
 //   p_j = e^{scale·q[s,h]·kv[idx_j] - m},  idx_j = -1 (or out of range) masked,
 //   lse[s,h] = log(Σ_j p_j + e^{sink_h - m}) + m.
 //
-// Design (one query row and up to 64 heads per workgroup of 8 waves: four
-// S^T/softmax "producer" waves and four P.V "consumer" waves, one of each per
-// SIMD, so the matrix cores of a SIMD alternate between the two roles):
+// Design (up to 64 heads of one query row at a time per workgroup of 8 waves:
+// four S^T/softmax "producer" waves and four P.V "consumer" waves, one of
+// each per SIMD, so the matrix cores of a SIMD alternate between the two
+// roles; at D >= 512 a workgroup takes 8 consecutive rows one after the other
+// and fetches each next row's first index words during the current row):
 //   * The row's top-k KV rows are gathered 32 at a time straight from L2/HBM
 //     into a 4-slot LDS ring with global_load_lds (no staging registers) by
 //     the producers, three tiles ahead of use; each row is read once per query
@@ -83,8 +85,21 @@ constexpr float kLazyRescaleF16 = 8.0f;
 // dealt round-robin), one of each per SIMD.
 constexpr int kAttnThreads = 2 * kAttnWaves * 64;
 
+// Query rows per workgroup (ROWS), handled one after the other: while a
+// row's last tiles run, the index wave copies the next row's first index
+// words, so each row after the first starts without waiting for them (half
+// of a row's prologue at D = 576).  Used where one workgroup fills a CU
+// (D >= 512); with several workgroups per CU the others hide the prologue
+// and a shorter grid only costs (measured: -3 % at D = 576, +27 % at D = 64
+// for 8 rows).
+template <int D>
+constexpr int attn_rows_per_workgroup() {
+  return D >= 512 ? 8 : 1;
+}
+
 template <int D, bool IDX64, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
+  constexpr int kAttnRows = attn_rows_per_workgroup<D>();
   using SH = AttnShape<D>;
   constexpr int KS = SH::KS;
   constexpr int MBW = SH::MBW;
@@ -106,445 +121,476 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   __builtin_assume(wave >= 0 && wave < kAttnWaves);  // lets per-copy bounds fold at compile time
   const int g = lane >> 4;     // lane group 0..3
   const int i16 = lane & 15;
-  const int s = blockIdx.x % a.S;
-  const int rest = blockIdx.x / a.S;
+  const int nsg = (a.S + kAttnRows - 1) / kAttnRows;  // row groups
+  const int sg = blockIdx.x % nsg;
+  const int rest = blockIdx.x / nsg;
   const int b = rest % a.B;
   const int hg = rest / a.B;
   const int hbase = hg * 64;
-  // Columns of this row: K, or fewer when a row length is given (the rest
-  // are masked and their tiles never run).  With no KV rows every key is
-  // masked: the tile loop is skipped.
-  int klen = a.K;
-  if (a.row_len) {
-    const int rl = a.row_len[b * a.rlsb + static_cast<int64_t>(s) * a.rlss];
-    klen = rl < 0 ? 0 : (rl < a.K ? rl : a.K);
-  }
-  const int ntiles = a.N > 0 ? (klen + kAttnTK - 1) / kAttnTK : 0;
-
-  // Tile protocol (one barrier per tile).  Iteration `it`: the consumers
-  // compute P.V of tile it while the producers compute S^T + softmax of tile
-  // it+1 and publish its P^T and rescale factors; tile t lives in ring slot
-  // t % 4 and its P^T in p_lds[t % 2].  The producers issue the copies of
-  // tile it+3 at the start of the iteration into the slot of tile it-1
-  // (finished by every wave in iteration it-1); they must land by the end of
-  // iteration it+1, two iterations of gather latency.  The first consumer
-  // wave copies the raw indices of tile it+6 at the start and publishes those
-  // of tile it+5 (copied one iteration earlier) before the barrier.
-
-  if (producer) {
-    // ======================= S^T + online softmax ==========================
-    const int hq = hbase + wave * 16 + i16;  // this lane's head
-    const bool hvalid = hq < a.H;
-    bf16x8 qf[KS];
-    {
-      const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
+  // Columns of row r: K, or fewer when a row length is given (the rest are
+  // masked and their tiles never run).  With no KV rows every key is masked:
+  // the tile loop is skipped.
+  auto row_klen = [&](int r) {
+    int kl = a.K;
+    if (a.row_len) {
+      const int rl = a.row_len[b * a.rlsb + static_cast<int64_t>(r) * a.rlss];
+      kl = rl < 0 ? 0 : (rl < a.K ? rl : a.K);
     }
+    return kl;
+  };
+  const char* idx_base = static_cast<const char*>(a.idx) + b * a.isb * (IDX64 ? 8 : 4);
+  bool idx_ready = false;  // (index wave) this row's first index words were copied during the previous row
+  for (int jr = 0; jr < kAttnRows; ++jr) {
+    const int s = sg * kAttnRows + jr;
+    if (s >= a.S) break;
+    const int klen = row_klen(s);
+    const int ntiles = a.N > 0 ? (klen + kAttnTK - 1) / kAttnTK : 0;
+    const int s_nx = (jr + 1 < kAttnRows && s + 1 < a.S) ? s + 1 : -1;
+    const int klen_nx = s_nx >= 0 ? row_klen(s_nx) : 0;
+    const int ntiles_nx = (s_nx >= 0 && a.N > 0) ? (klen_nx + kAttnTK - 1) / kAttnTK : 0;
 
-    // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
-    // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
-    // offset is a per-lane base (one per ks parity) plus 64 ks + 16 ROW mb.
-    const int qf_swz = kv_swz<D>(i16);
-    const int qbase = i16 * ROW + 16 * (g ^ (qf_swz & 3));
-    const int qadj = 64 * (qf_swz >> 2);
-    float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
-    float l_run = 0.f;       // this lane's share of the denominator
+    // Tile protocol (one barrier per tile).  Iteration `it`: the consumers
+    // compute P.V of tile it while the producers compute S^T + softmax of tile
+    // it+1 and publish its P^T and rescale factors; tile t lives in ring slot
+    // t % 4 and its P^T in p_lds[t % 2].  The producers issue the copies of
+    // tile it+3 at the start of the iteration into the slot of tile it-1
+    // (finished by every wave in iteration it-1); they must land by the end of
+    // iteration it+1, two iterations of gather latency.  The first consumer
+    // wave copies the raw indices of tile it+6 at the start and publishes those
+    // of tile it+5 (copied one iteration earlier) before the barrier.
 
-    // ---- KV gather (issued by the producers, which wait at the tile barrier
-    // for the P.V waves otherwise) -------------------------------------------
-    const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
-    // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
-    // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
-    // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
-    // source is kv + 16 (rowoff16[key] + dcoff).
-    int dkey[SH::LPT], dcoff[SH::LPT];
-#pragma unroll
-    for (int i = 0; i < SH::LPT; ++i) {
-      const int e = i * SH::NT + static_cast<int>(threadIdx.x);
-      dkey[i] = e / SH::CPR;
-      dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
-    }
-    uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
-    auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
-      const int slot = t % kAttnRing;
-#pragma unroll
-      for (int i = 0; i < SH::LPT; ++i)
-        dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
-    };
-    // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
-    // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
-    auto dma = [&](int t, auto IC) {
-      constexpr int i = decltype(IC)::value;
-      const int e0 = i * SH::NT + wave * 64;
-      char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
-      // (passed as uint16_t*: a char* argument to this builtin makes clang
-      // drop the host launch stubs of later instantiations)
-      const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
-      if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-      } else if (e0 < SH::CH) {
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
-      }
-    };
-    // The copies of tile `src` (its row offsets) into the ring slot of tile `dst`.
-    auto issue_tile_from = [&](int src, int dst) {
-      read_roff(src, roff);
-      attn_static_for<0, SH::LPT>([&](auto IC) { dma(dst, IC); });
-    };
-
-
-    // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
-    // A-fragments stream through a QPD-deep register queue: each MFMA's
-    // operand was read from LDS QPD k-steps earlier.
-    constexpr int QPD = KS < 4 ? KS : 4;
-    auto qk = [&](int t, f32x4 (&st)[2]) {
-      const uint32_t tile = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE);
-      const uint32_t qa_e = tile + qbase + qadj;
-      const uint32_t qa_o = tile + qbase - qadj;
-      bf16x8 kq[QPD][2];
-      auto qk_issue = [&](auto KC) {
-        constexpr int ks = decltype(KC)::value;
-        const uint32_t base = (ks & 1) ? qa_o : qa_e;
-        kq[ks % QPD][0] = ld128<64 * ks>(base);
-        kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
-      };
-      attn_static_for<0, QPD>(qk_issue);
-      st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      auto qk_step = [&](auto KC) {
-        constexpr int ks = decltype(KC)::value;
-        constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
-        lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
-        st[0] = mfma16x16x32<F16>(kq[ks % QPD][0], qf[ks], st[0]);
-        st[1] = mfma16x16x32<F16>(kq[ks % QPD][1], qf[ks], st[1]);
-        if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
-      };
-      attn_static_for<0, KS>(qk_step);
-      mfma_result_fence(st[0], st[1]);
-    };
-
-    // Online softmax of tile t for head hq, in registers; the result (P^T as
-    // a bf16 B-fragment and the head's rescale factor) is published by
-    // softmax_store.
-    struct SoftmaxOut {
-      u32x4 w;
-      float alpha;
-    };
-    auto softmax = [&](const f32x4 (&st)[2], const f32x4 (&bias)[2]) {
-      SoftmaxOut out;
-      float x[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
-      // tile maximum: in-lane, then over the lane groups g ^ 1 and g ^ 2
-      float tmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0][0], x[0][1]), __builtin_fmaxf(x[0][2], x[0][3])),
-                                   __builtin_fmaxf(__builtin_fmaxf(x[1][0], x[1][1]), __builtin_fmaxf(x[1][2], x[1][3])));
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-      tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-      const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
-      tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
-      // First valid key of the head: the accumulator and denominator are
-      // still zero, so the reference moves without a rescale (alpha = 1).
-      const bool first = m_ref == -1.0e30f;
-      const bool raise = first ? tmax > m_ref : tmax > m_ref + (F16 ? kLazyRescaleF16 : kLazyRescale);
-      const float m_new = raise ? tmax : m_ref;
-      out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
-      m_ref = m_new;
-      f32x2 p[4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        p[2 * mb] = f32x2{__builtin_amdgcn_exp2f(x[mb][0] - m_ref), __builtin_amdgcn_exp2f(x[mb][1] - m_ref)};
-        p[2 * mb + 1] = f32x2{__builtin_amdgcn_exp2f(x[mb][2] - m_ref), __builtin_amdgcn_exp2f(x[mb][3] - m_ref)};
-      }
-      const float psum = ((p[0][0] + p[0][1]) + (p[1][0] + p[1][1])) + ((p[2][0] + p[2][1]) + (p[3][0] + p[3][1]));
-      l_run = l_run * out.alpha + psum;
-      // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
-#pragma unroll
-      for (int c = 0; c < 4; ++c) out.w[c] = pack2<F16>(p[c][0], p[c][1]);
-      return out;
-    };
-    // (inline asm: the compiler makes a tracked LDS access that follows
-    // LDS-DMA copies wait for all of them; the tile barrier's lgkmcnt(0)
-    // orders these stores)
-    auto softmax_store = [&](int t, const SoftmaxOut& r, bool live) {
-      const uint32_t pa = lds_addr(&p_lds[t & 1][(wave * 64 + lane) * 16]);
-      asm volatile("ds_write_b128 %0, %1" ::"v"(pa), "v"(r.w) : "memory");
-      if (g == 0) {
-        const uint32_t aa = lds_addr(reinterpret_cast<const char*>(&alpha_lds[t & 1][wave * 16 + i16]));
-        asm volatile("ds_write_b32 %0, %1" ::"v"(aa), "v"(r.alpha) : "memory");
-      }
-      if (wave == 0 && lane == 0) {
-        const uint32_t la = lds_addr(reinterpret_cast<const char*>(&live_lds[t & 1]));
-        asm volatile("ds_write_b32 %0, %1" ::"v"(la), "v"(live ? 1 : 0) : "memory");
-      }
-    };
-    // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r);
-    // the slot read is always inside the array, so no guard is needed.
-    auto read_bias = [&](int t, f32x4 (&bias)[2]) {
-      bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
-      bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
-    };
-    // Whether any key of the tile is valid (wave-uniform): the four lane
-    // groups' biases cover all 32 keys.  An all-masked tile needs no S^T (its
-    // scores are 0 + bias = -inf either way) and no P.V (P = 0).
-    auto tile_live = [&](const f32x4 (&bias)[2]) {
-      bool any = false;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) any |= (bias[0][r] == 0.f) | (bias[1][r] == 0.f);
-      return __builtin_amdgcn_ballot_w64(any) != 0;
-    };
-    const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    if (ntiles > 0) {
-      // (prologue barriers without a release fence, like the tile barrier: a
-      // fence would make the compiler wait here for the Q loads and for every
-      // tile copy in flight, not just the ones the comments name)
-      attn_tile_barrier();  // indices of tiles 0..3 published
-      // Copies of tiles 0, 1 and 2.  A row with fewer tiles copies its last
-      // tile again into the slots it does not use, so every row waits the same
-      // way and the compiler sees that the Q loads (issued first) have landed
-      // once tile 0 has.
-      issue_tile_from(0, 0);
-      issue_tile_from(ntiles > 1 ? 1 : ntiles - 1, 1);
-      issue_tile_from(ntiles > 2 ? 2 : ntiles - 1, 2);
-      // tile 0 (and every Q load) landed; the copies of tiles 1 and 2 may still be in flight
-      __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
-      attn_tile_barrier();  // tile 0 landed
-      f32x4 bias_cur[2];
+    if (producer) {
+      // ======================= S^T + online softmax ==========================
+      const int hq = hbase + wave * 16 + i16;  // this lane's head
+      const bool hvalid = hq < a.H;
+      bf16x8 qf[KS];
       {
-        f32x4 bias[2], st[2] = {zero4, zero4};
-        read_bias(0, bias);
-        read_bias(1, bias_cur);
-        read_roff(3, roff);
-        const bool live = tile_live(bias);
-        if (live) qk(0, st);
-        softmax_store(0, softmax(st, bias), live);
+        const uint16_t* qrow = a.q + b * a.qsb + static_cast<int64_t>(s) * a.qss + static_cast<int64_t>(hq) * a.qsh;
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          qf[ks] = hvalid ? *reinterpret_cast<const bf16x8*>(qrow + ks * 32 + g * 8) : bf16x8{};
       }
-      // tile 1 landed; the copies of tile 2 may still be in flight
-      __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-      attn_tile_barrier();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
-      attn_tile_barrier();  // indices of tile 4 published
-      uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
-      for (int it = 0; it < ntiles; ++it) {
-        const bool issue = it + 3 < ntiles;
-        // tracked LDS reads first, then the copies of tile it+3 into the slot
-        // of tile it-1 (finished by every wave in iteration it-1)
-        f32x4 bias_nx[2];
-        read_bias(it + 2, bias_nx);    // slots read are always inside the arrays
-        read_roff(it + 4, roff_nx);
-        if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
-        if (it + 1 < ntiles) {
-          f32x4 st[2] = {zero4, zero4};
-          const bool live = tile_live(bias_cur);
-          if (live) qk(it + 1, st);
-          softmax_store(it + 1, softmax(st, bias_cur), live);
-        }
-        bias_cur[0] = bias_nx[0];
-        bias_cur[1] = bias_nx[1];
-#pragma unroll
-        for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
-        // the copies of tile it+2 (issued one iteration ago) landed; those of
-        // tile it+3 stay in flight across the barrier
-        if (issue) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
-        else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-        attn_tile_barrier();
-      }
-    }
 
-    // ---- denominators, sink, normalisation factor, lse ----------------------
-    float l_tot;
-    {  // sum over the four lane groups
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-      l_tot = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-      const SwapPair r32 = permlane32_swap(__float_as_uint(l_tot), __float_as_uint(l_tot));
-      l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
-    }
-    constexpr float kLog2e = 1.4426950408889634f;
-    // (the sink is read only now: a load at the top would make the first
-    // copies wait for every Q load)
-    const float sink_v = hvalid ? a.sink[hq] : 0.f;
-    const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
-    const float m_fin = __builtin_fmaxf(m_ref, sink2);
-    const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
-    const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
-    const float scale = l_fin > 0.f ? resc / l_fin : 0.f;
-    if (g == 0) {
-      scale_lds[wave * 16 + i16] = scale;
-      if (hvalid) {
-        constexpr float kLn2 = 0.6931471805599453f;
-        const float lse = l_fin > 0.f ? (__builtin_amdgcn_logf(l_fin) + m_fin) * kLn2 : -1.0e30f;
-        a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(hq) * a.lsh] = lse;
-      }
-    }
-    __syncthreads();  // normalisation factors published
-    __syncthreads();  // output staged
-  } else {
-    // ============== P.V, KV gather and the index pipeline =====================
-    const bool idx_wave = wave == 0;
-    const char* idx_row = static_cast<const char*>(a.idx) +
-                          (b * a.isb + static_cast<int64_t>(s) * a.iss) * (IDX64 ? 8 : 4);
+      // S^T A-fragment addresses: key 16mb + i16, chunk 4ks + g.  With
+      // f = kv_swz(i16), (4ks + g) ^ f = 4 (ks ^ (f >> 2)) + (g ^ (f & 3)), so the
+      // offset is a per-lane base (one per ks parity) plus 64 ks + 16 ROW mb.
+      const int qf_swz = kv_swz<D>(i16);
+      const int qbase = i16 * ROW + 16 * (g ^ (qf_swz & 3));
+      const int qadj = 64 * (qf_swz >> 2);
+      float m_ref = -1.0e30f;  // reference maximum of this lane's head (log2 domain)
+      float l_run = 0.f;       // this lane's share of the denominator
 
-    // Key indices of tile `t`: the index wave copies the raw index words into
-    // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
-    // no loop-carried load result forces an early wait), and after its next
-    // full wait reads them back, validates them and publishes validity and
-    // row offsets to ring slot t % 4 for every wave.
-    auto load_idx = [&](int t) {
-      // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
-      int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
-      j = j < klen ? j : klen - 1;  // klen > 0 whenever a tile exists
-      const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(idx_row + byte),
-                                       (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
-    };
-    auto store_idx = [&](int t) {
-      const int slot = t % kAttnRing;
-      const int rslot = t % (2 * kAttnRing);
-      if (lane < kAttnTK) {
-        const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
-                                                         idxraw_lds[rslot][2 * lane])
-                                  : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
-        const int j = t * kAttnTK + lane;
-        const bool ok = j < klen && raw >= 0 && raw < a.N;
-        bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
-        rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
+      // ---- KV gather (issued by the producers, which wait at the tile barrier
+      // for the P.V waves otherwise) -------------------------------------------
+      const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+      // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
+      // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
+      // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
+      // source is kv + 16 (rowoff16[key] + dcoff).
+      int dkey[SH::LPT], dcoff[SH::LPT];
+  #pragma unroll
+      for (int i = 0; i < SH::LPT; ++i) {
+        const int e = i * SH::NT + static_cast<int>(threadIdx.x);
+        dkey[i] = e / SH::CPR;
+        dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
       }
-    };
-    // V^T transposing-read address: source lane (g, i16) points at key
-    // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
-    // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
-    // swizzles to 8j + (x ^ f), so block j is at a fixed base + 128 j.
-    const int tkey = 4 * g + (i16 >> 2);
-    const int tx = 2 * wave + ((i16 & 3) >> 1);
-    const int tbase = tkey * ROW + 16 * ((tx ^ kv_swz<D>(tkey)) & (SH::CPR - 1)) + 8 * (i16 & 1);
-
-    f32x4 oacc[MBW][4];
-#pragma unroll
-    for (int j = 0; j < MBW; ++j)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // O^T += V^T P^T of tile `it` for this wave's 16-dim blocks and all 64
-    // heads.  The P^T fragments and the V^T blocks are read from inline asm
-    // with exact waits: blocks j and j+1 are in flight while block j's MFMAs
-    // run (LDS operations complete in order, so waiting for "at most 2
-    // outstanding" covers everything issued before block j+1).
-    auto pv = [&](int it) {
-      const uint32_t pa = lds_addr(&p_lds[it & 1][0]) + lane * 16;
-      bf16x8 pbr[4];
-      pbr[0] = ld128<0>(pa);
-      pbr[1] = ld128<1024>(pa);
-      pbr[2] = ld128<2048>(pa);
-      pbr[3] = ld128<3072>(pa);
-      const uint32_t ta = lds_addr(kv_lds + (it % kAttnRing) * SH::TILE) + tbase;
-      v4i16 lo[2], hi[2];
-      lo[0] = tr_read<0>(ta);
-      hi[0] = tr_read<16 * ROW>(ta);
-      if constexpr (MBW > 1) {
-        lo[1] = tr_read<128>(ta);
-        hi[1] = tr_read<16 * ROW + 128>(ta);
-      }
-      auto block = [&](auto JC) {
-        constexpr int j = decltype(JC)::value;
-        if constexpr (j + 1 < MBW) lds_wait<2>(lo[j & 1], hi[j & 1]); else lds_wait<0>(lo[j & 1], hi[j & 1]);
-        if constexpr (j == 0) {
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb) reg_tie(pbr[nb]);
-        }
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j & 1], hi[j & 1], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = mfma16x16x32<F16>(vf, pbr[nb], oacc[j][nb]);
-        if constexpr (j + 2 < MBW) {
-          lo[j & 1] = tr_read<128 * (j + 2)>(ta);
-          hi[j & 1] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
+      uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
+      auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
+        const int slot = t % kAttnRing;
+  #pragma unroll
+        for (int i = 0; i < SH::LPT; ++i)
+          dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+      };
+      // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
+      // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
+      auto dma = [&](int t, auto IC) {
+        constexpr int i = decltype(IC)::value;
+        const int e0 = i * SH::NT + wave * 64;
+        char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
+        // (passed as uint16_t*: a char* argument to this builtin makes clang
+        // drop the host launch stubs of later instantiations)
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+        if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
+          __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
+        } else if (e0 < SH::CH) {
+          __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
         }
       };
-      attn_static_for<0, MBW>(block);
-    };
+      // The copies of tile `src` (its row offsets) into the ring slot of tile `dst`.
+      auto issue_tile_from = [&](int src, int dst) {
+        read_roff(src, roff);
+        attn_static_for<0, SH::LPT>([&](auto IC) { dma(dst, IC); });
+      };
 
-    // One consumer iteration: P.V of tile it and the index pipeline.
-    auto iteration = [&](int it) {
-      float al[4];
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
-      // wave-uniform in a scalar register, so the skip is a scalar branch
-      // (MFMAs do not honour EXEC)
-      const bool live = __builtin_amdgcn_readfirstlane(live_lds[it & 1]) != 0;
-      if (idx_wave && it + 6 < ntiles) load_idx(it + 6);
-      const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
-                                                           al[3] != 1.0f) != 0;
-      if (__builtin_expect(any_rescale, 0)) {
-#pragma unroll
-        for (int j = 0; j < MBW; ++j)
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
-      }
-      if (live) pv(it);  // P = 0 for a tile without a valid key
-      // the indices of tile it+5 (copied one iteration ago) landed; in the
-      // index wave those of tile it+6 may stay in flight
-      if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(1));
-      else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
-      if (idx_wave && it + 5 < ntiles) store_idx(it + 5);
-    };
 
-    if (ntiles > 0) {
-      // indices of tiles 0..5; tile 4 shares its row-offset / bias slot with
-      // tile 0, so it is published once tile 0's entries have been read, and
-      // tile 5 at the end of iteration 0
-      if (idx_wave) {
-        const int np = ntiles < 6 ? ntiles : 6;
-        for (int t = 0; t < np; ++t) load_idx(t);
-        __builtin_amdgcn_s_waitcnt(0x7 << 4);
-        for (int t = 0; t < np && t < 4; ++t) store_idx(t);
-      }
-      __syncthreads();  // indices of tiles 0..3 published
-      __syncthreads();  // tile 0 landed
-      __syncthreads();  // tile 1 landed; every wave has read tile 0's row offsets and biases
-      if (idx_wave && ntiles > 4) store_idx(4);
-      __syncthreads();  // indices of tile 4 published
-      for (int it = 0; it < ntiles; ++it) {
-        iteration(it);
-        attn_tile_barrier();  // (store_idx's LDS stores complete first)
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
-    __syncthreads();  // normalisation factors published
-    // Normalised O (bf16) staged head-major in LDS: [64 heads][OROW bytes].
-    float sc[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) sc[nb] = scale_lds[nb * 16 + i16];
-#pragma unroll
-    for (int j = 0; j < MBW; ++j) {
-      const int mbi = j * kAttnWaves + wave;
-      if (SH::MBT % kAttnWaves == 0 || mbi < SH::MBT) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          uint2 w;
-          w.x = pack2<F16>(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
-          w.y = pack2<F16>(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
-          *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
+      // S^T = K Q^T of tile t for this wave's 16 heads (keys 16mb + 4g + r).
+      // A-fragments stream through a QPD-deep register queue: each MFMA's
+      // operand was read from LDS QPD k-steps earlier.
+      constexpr int QPD = KS < 4 ? KS : 4;
+      auto qk = [&](int t, f32x4 (&st)[2]) {
+        const uint32_t tile = lds_addr(kv_lds + (t % kAttnRing) * SH::TILE);
+        const uint32_t qa_e = tile + qbase + qadj;
+        const uint32_t qa_o = tile + qbase - qadj;
+        bf16x8 kq[QPD][2];
+        auto qk_issue = [&](auto KC) {
+          constexpr int ks = decltype(KC)::value;
+          const uint32_t base = (ks & 1) ? qa_o : qa_e;
+          kq[ks % QPD][0] = ld128<64 * ks>(base);
+          kq[ks % QPD][1] = ld128<64 * ks + 16 * ROW>(base);
+        };
+        attn_static_for<0, QPD>(qk_issue);
+        st[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto qk_step = [&](auto KC) {
+          constexpr int ks = decltype(KC)::value;
+          constexpr int later = (KS - 1 - ks) < (QPD - 1) ? (KS - 1 - ks) : (QPD - 1);  // k-steps issued after ks
+          lds_wait<2 * later>(kq[ks % QPD][0], kq[ks % QPD][1]);
+          st[0] = mfma16x16x32<F16>(kq[ks % QPD][0], qf[ks], st[0]);
+          st[1] = mfma16x16x32<F16>(kq[ks % QPD][1], qf[ks], st[1]);
+          if constexpr (ks + QPD < KS) qk_issue(std::integral_constant<int, ks + QPD>{});
+        };
+        attn_static_for<0, KS>(qk_step);
+        mfma_result_fence(st[0], st[1]);
+      };
+
+      // Online softmax of tile t for head hq, in registers; the result (P^T as
+      // a bf16 B-fragment and the head's rescale factor) is published by
+      // softmax_store.
+      struct SoftmaxOut {
+        u32x4 w;
+        float alpha;
+      };
+      auto softmax = [&](const f32x4 (&st)[2], const f32x4 (&bias)[2]) {
+        SoftmaxOut out;
+        float x[2][4];
+  #pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
+        // tile maximum: in-lane, then over the lane groups g ^ 1 and g ^ 2
+        float tmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0][0], x[0][1]), __builtin_fmaxf(x[0][2], x[0][3])),
+                                     __builtin_fmaxf(__builtin_fmaxf(x[1][0], x[1][1]), __builtin_fmaxf(x[1][2], x[1][3])));
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+        tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
+        tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+        // First valid key of the head: the accumulator and denominator are
+        // still zero, so the reference moves without a rescale (alpha = 1).
+        const bool first = m_ref == -1.0e30f;
+        const bool raise = first ? tmax > m_ref : tmax > m_ref + (F16 ? kLazyRescaleF16 : kLazyRescale);
+        const float m_new = raise ? tmax : m_ref;
+        out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
+        m_ref = m_new;
+        f32x2 p[4];
+  #pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          p[2 * mb] = f32x2{__builtin_amdgcn_exp2f(x[mb][0] - m_ref), __builtin_amdgcn_exp2f(x[mb][1] - m_ref)};
+          p[2 * mb + 1] = f32x2{__builtin_amdgcn_exp2f(x[mb][2] - m_ref), __builtin_amdgcn_exp2f(x[mb][3] - m_ref)};
+        }
+        const float psum = ((p[0][0] + p[0][1]) + (p[1][0] + p[1][1])) + ((p[2][0] + p[2][1]) + (p[3][0] + p[3][1]));
+        l_run = l_run * out.alpha + psum;
+        // P^T B-fragment: k-slots 8g+0..3 <-> keys 4g+0..3, 8g+4..7 <-> keys 16+4g+0..3
+  #pragma unroll
+        for (int c = 0; c < 4; ++c) out.w[c] = pack2<F16>(p[c][0], p[c][1]);
+        return out;
+      };
+      // (inline asm: the compiler makes a tracked LDS access that follows
+      // LDS-DMA copies wait for all of them; the tile barrier's lgkmcnt(0)
+      // orders these stores)
+      auto softmax_store = [&](int t, const SoftmaxOut& r, bool live) {
+        const uint32_t pa = lds_addr(&p_lds[t & 1][(wave * 64 + lane) * 16]);
+        asm volatile("ds_write_b128 %0, %1" ::"v"(pa), "v"(r.w) : "memory");
+        if (g == 0) {
+          const uint32_t aa = lds_addr(reinterpret_cast<const char*>(&alpha_lds[t & 1][wave * 16 + i16]));
+          asm volatile("ds_write_b32 %0, %1" ::"v"(aa), "v"(r.alpha) : "memory");
+        }
+        if (wave == 0 && lane == 0) {
+          const uint32_t la = lds_addr(reinterpret_cast<const char*>(&live_lds[t & 1]));
+          asm volatile("ds_write_b32 %0, %1" ::"v"(la), "v"(live ? 1 : 0) : "memory");
+        }
+      };
+      // Key biases of tile t in the score-accumulator order (keys 4g+r, 16+4g+r);
+      // the slot read is always inside the array, so no guard is needed.
+      auto read_bias = [&](int t, f32x4 (&bias)[2]) {
+        bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
+        bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
+      };
+      // Whether any key of the tile is valid (wave-uniform): the four lane
+      // groups' biases cover all 32 keys.  An all-masked tile needs no S^T (its
+      // scores are 0 + bias = -inf either way) and no P.V (P = 0).
+      auto tile_live = [&](const f32x4 (&bias)[2]) {
+        bool any = false;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) any |= (bias[0][r] == 0.f) | (bias[1][r] == 0.f);
+        return __builtin_amdgcn_ballot_w64(any) != 0;
+      };
+      const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+
+      if (ntiles > 0) {
+        // (prologue barriers without a release fence, like the tile barrier: a
+        // fence would make the compiler wait here for the Q loads and for every
+        // tile copy in flight, not just the ones the comments name)
+        attn_tile_barrier();  // indices of tiles 0..3 published
+        // Copies of tiles 0, 1 and 2.  A row with fewer tiles copies its last
+        // tile again into the slots it does not use, so every row waits the same
+        // way and the compiler sees that the Q loads (issued first) have landed
+        // once tile 0 has.
+        issue_tile_from(0, 0);
+        issue_tile_from(ntiles > 1 ? 1 : ntiles - 1, 1);
+        issue_tile_from(ntiles > 2 ? 2 : ntiles - 1, 2);
+        // tile 0 (and every Q load) landed; the copies of tiles 1 and 2 may still be in flight
+        __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
+        attn_tile_barrier();  // tile 0 landed
+        f32x4 bias_cur[2];
+        {
+          f32x4 bias[2], st[2] = {zero4, zero4};
+          read_bias(0, bias);
+          read_bias(1, bias_cur);
+          read_roff(3, roff);
+          const bool live = tile_live(bias);
+          if (live) qk(0, st);
+          softmax_store(0, softmax(st, bias), live);
+        }
+        // tile 1 landed; the copies of tile 2 may still be in flight
+        __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+        attn_tile_barrier();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
+        attn_tile_barrier();  // indices of tile 4 published
+        uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
+        for (int it = 0; it < ntiles; ++it) {
+          const bool issue = it + 3 < ntiles;
+          // tracked LDS reads first, then the copies of tile it+3 into the slot
+          // of tile it-1 (finished by every wave in iteration it-1)
+          f32x4 bias_nx[2];
+          read_bias(it + 2, bias_nx);    // slots read are always inside the arrays
+          read_roff(it + 4, roff_nx);
+          if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
+          if (it + 1 < ntiles) {
+            f32x4 st[2] = {zero4, zero4};
+            const bool live = tile_live(bias_cur);
+            if (live) qk(it + 1, st);
+            softmax_store(it + 1, softmax(st, bias_cur), live);
+          }
+          bias_cur[0] = bias_nx[0];
+          bias_cur[1] = bias_nx[1];
+  #pragma unroll
+          for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
+          // the copies of tile it+2 (issued one iteration ago) landed; those of
+          // tile it+3 stay in flight across the barrier
+          if (issue) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
+          else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+          attn_tile_barrier();
         }
       }
-    }
-    __syncthreads();  // output staged
-  }
 
-  // ---- coalesced 16-byte stores of the staged output (all threads) ---------
-  const int hcount = (a.H - hbase) < 64 ? (a.H - hbase) : 64;
-  uint16_t* obase = a.o + b * a.osb + static_cast<int64_t>(s) * a.oss + static_cast<int64_t>(hbase) * a.osh;
-  for (int e = threadIdx.x; e < hcount * SH::CPR; e += kAttnThreads) {
-    const int h = e / SH::CPR, c = e % SH::CPR;
-    *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(h) * a.osh + c * 8) =
-        *reinterpret_cast<const u32x4*>(kv_lds + h * SH::OROW + c * 16);
+      // ---- denominators, sink, normalisation factor, lse ----------------------
+      float l_tot;
+      {  // sum over the four lane groups
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+        l_tot = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+        const SwapPair r32 = permlane32_swap(__float_as_uint(l_tot), __float_as_uint(l_tot));
+        l_tot = __uint_as_float(r32.x) + __uint_as_float(r32.y);
+      }
+      constexpr float kLog2e = 1.4426950408889634f;
+      // (the sink is read only now: a load at the top would make the first
+      // copies wait for every Q load)
+      const float sink_v = hvalid ? a.sink[hq] : 0.f;
+      const float sink2 = hvalid ? sink_v * kLog2e : -__builtin_inff();
+      const float m_fin = __builtin_fmaxf(m_ref, sink2);
+      const float resc = __builtin_amdgcn_exp2f(m_ref - m_fin);
+      const float l_fin = l_tot * resc + __builtin_amdgcn_exp2f(sink2 - m_fin);
+      const float scale = l_fin > 0.f ? resc / l_fin : 0.f;
+      if (g == 0) {
+        scale_lds[wave * 16 + i16] = scale;
+        if (hvalid) {
+          constexpr float kLn2 = 0.6931471805599453f;
+          const float lse = l_fin > 0.f ? (__builtin_amdgcn_logf(l_fin) + m_fin) * kLn2 : -1.0e30f;
+          a.lse[b * a.lsb + static_cast<int64_t>(s) * a.lss + static_cast<int64_t>(hq) * a.lsh] = lse;
+        }
+      }
+      __syncthreads();  // normalisation factors published
+      __syncthreads();  // output staged
+    } else {
+      // ============== P.V, KV gather and the index pipeline =====================
+      const bool idx_wave = wave == 0;
+      const char* idx_row = idx_base + static_cast<int64_t>(s) * a.iss * (IDX64 ? 8 : 4);
+      const char* idx_row_nx = idx_base + static_cast<int64_t>(s_nx < 0 ? 0 : s_nx) * a.iss * (IDX64 ? 8 : 4);
+
+      // Key indices of tile `t`: the index wave copies the raw index words into
+      // idxraw_lds[t % 8] with a global_load_lds (nothing lands in registers, so
+      // no loop-carried load result forces an early wait), and after its next
+      // full wait reads them back, validates them and publishes validity and
+      // row offsets to ring slot t % 4 for every wave.
+      auto load_idx_of = [&](const char* row, int kl, int t) {
+        // 64-bit indices: lane l copies word l & 1 of key l >> 1; 32-bit: key l & 31.
+        int j = t * kAttnTK + (IDX64 ? (lane >> 1) : (lane & 31));
+        j = j < kl ? j : kl - 1;  // kl > 0 whenever a tile exists
+        const int64_t byte = static_cast<int64_t>(j) * a.isk * (IDX64 ? 8 : 4) + (IDX64 ? (lane & 1) * 4 : 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(row + byte),
+                                         (lds_void_t*)(&idxraw_lds[t % (2 * kAttnRing)][0]), 4, 0, 0);
+      };
+      auto load_idx = [&](int t) { load_idx_of(idx_row, klen, t); };
+      // The next row's first index words go out once this row's index work is
+      // done (its last copy was waited for and its last publish read the raw
+      // slots one iteration earlier).
+      const int it_nx = ntiles > 5 ? ntiles - 5 : 0;
+      const int np_nx = ntiles_nx < 6 ? ntiles_nx : 6;
+      auto store_idx = [&](int t) {
+        const int slot = t % kAttnRing;
+        const int rslot = t % (2 * kAttnRing);
+        if (lane < kAttnTK) {
+          const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
+                                                           idxraw_lds[rslot][2 * lane])
+                                    : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
+          const int j = t * kAttnTK + lane;
+          const bool ok = j < klen && raw >= 0 && raw < a.N;
+          bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
+          rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
+        }
+      };
+      // V^T transposing-read address: source lane (g, i16) points at key
+      // 4g + (i16 >> 2) (+16 for k-slots 4..7), dims d0 + 4 (i16 & 3) with
+      // d0 = 16 (4j + wave); the chunk 8j + x, x = 2 wave + ((i16 & 3) >> 1) < 8,
+      // swizzles to 8j + (x ^ f), so block j is at a fixed base + 128 j.
+      const int tkey = 4 * g + (i16 >> 2);
+      const int tx = 2 * wave + ((i16 & 3) >> 1);
+      const int tbase = tkey * ROW + 16 * ((tx ^ kv_swz<D>(tkey)) & (SH::CPR - 1)) + 8 * (i16 & 1);
+
+      f32x4 oacc[MBW][4];
+  #pragma unroll
+      for (int j = 0; j < MBW; ++j)
+  #pragma unroll
+        for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+      // O^T += V^T P^T of tile `it` for this wave's 16-dim blocks and all 64
+      // heads.  The P^T fragments and the V^T blocks are read from inline asm
+      // with exact waits: blocks j and j+1 are in flight while block j's MFMAs
+      // run (LDS operations complete in order, so waiting for "at most 2
+      // outstanding" covers everything issued before block j+1).
+      auto pv = [&](int it) {
+        const uint32_t pa = lds_addr(&p_lds[it & 1][0]) + lane * 16;
+        bf16x8 pbr[4];
+        pbr[0] = ld128<0>(pa);
+        pbr[1] = ld128<1024>(pa);
+        pbr[2] = ld128<2048>(pa);
+        pbr[3] = ld128<3072>(pa);
+        const uint32_t ta = lds_addr(kv_lds + (it % kAttnRing) * SH::TILE) + tbase;
+        v4i16 lo[2], hi[2];
+        lo[0] = tr_read<0>(ta);
+        hi[0] = tr_read<16 * ROW>(ta);
+        if constexpr (MBW > 1) {
+          lo[1] = tr_read<128>(ta);
+          hi[1] = tr_read<16 * ROW + 128>(ta);
+        }
+        auto block = [&](auto JC) {
+          constexpr int j = decltype(JC)::value;
+          if constexpr (j + 1 < MBW) lds_wait<2>(lo[j & 1], hi[j & 1]); else lds_wait<0>(lo[j & 1], hi[j & 1]);
+          if constexpr (j == 0) {
+  #pragma unroll
+            for (int nb = 0; nb < 4; ++nb) reg_tie(pbr[nb]);
+          }
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo[j & 1], hi[j & 1], 0, 1, 2, 3, 4, 5, 6, 7));
+  #pragma unroll
+          for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = mfma16x16x32<F16>(vf, pbr[nb], oacc[j][nb]);
+          if constexpr (j + 2 < MBW) {
+            lo[j & 1] = tr_read<128 * (j + 2)>(ta);
+            hi[j & 1] = tr_read<16 * ROW + 128 * (j + 2)>(ta);
+          }
+        };
+        attn_static_for<0, MBW>(block);
+      };
+
+      // One consumer iteration: P.V of tile it and the index pipeline.
+      auto iteration = [&](int it) {
+        float al[4];
+  #pragma unroll
+        for (int nb = 0; nb < 4; ++nb) al[nb] = alpha_lds[it & 1][nb * 16 + i16];
+        // wave-uniform in a scalar register, so the skip is a scalar branch
+        // (MFMAs do not honour EXEC)
+        const bool live = __builtin_amdgcn_readfirstlane(live_lds[it & 1]) != 0;
+        if (idx_wave && it + 6 < ntiles) load_idx(it + 6);
+        if (idx_wave && it == it_nx) {
+          for (int t = 0; t < np_nx; ++t) load_idx_of(idx_row_nx, klen_nx, t);
+        }
+
+        const bool any_rescale = __builtin_amdgcn_ballot_w64(al[0] != 1.0f || al[1] != 1.0f || al[2] != 1.0f ||
+                                                             al[3] != 1.0f) != 0;
+        if (__builtin_expect(any_rescale, 0)) {
+  #pragma unroll
+          for (int j = 0; j < MBW; ++j)
+  #pragma unroll
+            for (int nb = 0; nb < 4; ++nb) oacc[j][nb] = oacc[j][nb] * al[nb];
+        }
+        if (live) pv(it);  // P = 0 for a tile without a valid key
+        // the indices of tile it+5 (copied one iteration ago) landed; in the
+        // index wave those of tile it+6 may stay in flight
+        if (idx_wave && it + 6 < ntiles) __builtin_amdgcn_s_waitcnt(vm_lgkm0(1));
+        else if (idx_wave && it >= it_nx && np_nx > 0)
+          __builtin_amdgcn_s_waitcnt(vm_lgkm0(63));  // (the next row's index words stay in flight)
+        else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
+        if (idx_wave && it + 5 < ntiles) store_idx(it + 5);
+      };
+
+      if (ntiles > 0) {
+        // indices of tiles 0..5; tile 4 shares its row-offset / bias slot with
+        // tile 0, so it is published once tile 0's entries have been read, and
+        // tile 5 at the end of iteration 0
+        if (idx_wave) {
+          const int np = ntiles < 6 ? ntiles : 6;
+          if (!idx_ready)
+            for (int t = 0; t < np; ++t) load_idx(t);
+          __builtin_amdgcn_s_waitcnt(0x7 << 4);
+          for (int t = 0; t < np && t < 4; ++t) store_idx(t);
+        }
+        __syncthreads();  // indices of tiles 0..3 published
+        __syncthreads();  // tile 0 landed
+        __syncthreads();  // tile 1 landed; every wave has read tile 0's row offsets and biases
+        if (idx_wave && ntiles > 4) store_idx(4);
+        __syncthreads();  // indices of tile 4 published
+        for (int it = 0; it < ntiles; ++it) {
+          iteration(it);
+          attn_tile_barrier();  // (store_idx's LDS stores complete first)
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x7 << 4);  // no gather may still target the ring
+      if (idx_wave) idx_ready = ntiles > 0 && np_nx > 0;
+      __syncthreads();  // normalisation factors published
+      // Normalised O (bf16) staged head-major in LDS: [64 heads][OROW bytes].
+      float sc[4];
+  #pragma unroll
+      for (int nb = 0; nb < 4; ++nb) sc[nb] = scale_lds[nb * 16 + i16];
+  #pragma unroll
+      for (int j = 0; j < MBW; ++j) {
+        const int mbi = j * kAttnWaves + wave;
+        if (SH::MBT % kAttnWaves == 0 || mbi < SH::MBT) {
+  #pragma unroll
+          for (int nb = 0; nb < 4; ++nb) {
+            uint2 w;
+            w.x = pack2<F16>(oacc[j][nb][0] * sc[nb], oacc[j][nb][1] * sc[nb]);
+            w.y = pack2<F16>(oacc[j][nb][2] * sc[nb], oacc[j][nb][3] * sc[nb]);
+            *reinterpret_cast<uint2*>(kv_lds + (nb * 16 + i16) * SH::OROW + (mbi * 16 + 4 * g) * 2) = w;
+          }
+        }
+      }
+      __syncthreads();  // output staged
+    }
+
+    // ---- coalesced 16-byte stores of the staged output (all threads) ---------
+    const int hcount = (a.H - hbase) < 64 ? (a.H - hbase) : 64;
+    uint16_t* obase = a.o + b * a.osb + static_cast<int64_t>(s) * a.oss + static_cast<int64_t>(hbase) * a.osh;
+    for (int e = threadIdx.x; e < hcount * SH::CPR; e += kAttnThreads) {
+      const int h = e / SH::CPR, c = e % SH::CPR;
+      *reinterpret_cast<u32x4*>(obase + static_cast<int64_t>(h) * a.osh + c * 8) =
+          *reinterpret_cast<const u32x4*>(kv_lds + h * SH::OROW + c * 16);
+    }
+    // (the next row's first barrier orders these reads of the staged output
+    // before its copies into the ring)
   }
 }
 
 template <int D>
 static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
-  const int64_t nblk = static_cast<int64_t>(a.B) * a.S * a.HG;
+  constexpr int R = attn_rows_per_workgroup<D>();
+  const int64_t nblk = static_cast<int64_t>(a.B) * ((a.S + R - 1) / R) * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
   const dim3 grid(static_cast<unsigned>(nblk)), block(kAttnThreads);
   if (a.f16) {
