@@ -185,6 +185,32 @@ def test_row_len(cuda_device, D, i64):
     assert o[:, 0].float().abs().max().item() == 0.0  # row_len 0: nothing attended
 
 
+@pytest.mark.parametrize("D", [576, 512])
+def test_rows_per_workgroup(cuda_device, D):
+    # At D >= 512 a workgroup runs 8 consecutive rows and copies each next row's
+    # first index words during the current row.  Rows of every kind next to each
+    # other in a group (no tile, one tile, five tiles -- the next row's words go
+    # out at the first iteration --, long rows, lengths past K), S not a multiple
+    # of 8, two batches and two head groups: bit for bit the same rows launched
+    # one at a time, and the oracle over the tail-masked rows.
+    B, S, H, N, K = 2, 37, 100, 400, 256
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=900 + D, q_scale=0.5, kv_scale=0.5)
+    g = torch.Generator().manual_seed(900 + D)
+    idx = torch.randint(-1, N, (B, S, K), generator=g, dtype=torch.int32)
+    rl = torch.randint(0, K + 40, (B, S), generator=g, dtype=torch.int32)
+    rl[:, :16] = torch.tensor([0, 0, 32, 160, 256, 1, 0, 300, 200, 33, 161, 0, 64, 256, 5, 129], dtype=torch.int32)
+    idx, rl = idx.cuda(), rl.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, D ** -0.5, row_len=rl)
+    torch.cuda.synchronize()
+    for s in range(S):
+        o1, l1 = sparse_attn_fwd(q[:, s:s + 1].contiguous(), kv, sink, idx[:, s:s + 1].contiguous(), D ** -0.5,
+                                 row_len=rl[:, s:s + 1].contiguous())
+        assert torch.equal(o[:, s:s + 1], o1) and torch.equal(lse[:, s:s + 1], l1), f"D={D} row {s}"
+    col = torch.arange(K, device="cuda")
+    masked = idx.masked_fill(col >= rl.unsqueeze(-1).long(), -1)
+    _check(q, kv, sink, masked, D ** -0.5, o, lse, f"rows per workgroup D={D}")
+
+
 @pytest.mark.parametrize("D", [32, 64, 128, 256, 512, 576])
 def test_head_dims(cuda_device, D):
     B, S, H, N, K = 1, 24, 64, 300, 96
