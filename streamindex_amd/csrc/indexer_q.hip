@@ -217,17 +217,26 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
   wait_vm_lgkm0<0>();
   __syncthreads();
 
-  for (int it = 0; it < ntiles; ++it) {
+  // Scale of this lane's key in the current tile: a pointer advanced by one
+  // tile per step (one 64-bit add instead of a multiply); keys past T (only in
+  // the tile that crosses T) read the last key's scale, as before.
+  const float* ksp = kscb + static_cast<int64_t>(okey) * a.kcst;
+  const int64_t kstep = static_cast<int64_t>(TILE_N) * a.kcst;
+  // One tile; SLOT (the ring slot of tile it) is a compile-time constant, so
+  // every LDS address of the tile is a per-lane base plus an immediate.
+  auto tile_step = [&](const int it, auto SLOTC) {
+    constexpr int slot = decltype(SLOTC)::value;
     const int tbase = it * TILE_N;
     const int t = tbase + okey;
     // per-lane loads of this tile (the key's scale and mask byte) first, so the
     // waits below cover the tile copies after them
-    const float kscale = kscb[static_cast<int64_t>(t < a.T ? t : a.T - 1) * a.kcst];
+    const float kscale = *(t < a.T ? ksp : kscb + static_cast<int64_t>(a.T - 1) * a.kcst);  // (always a valid address)
+    ksp += kstep;
     bool mok = true;
     if constexpr (MASKED) mok = t < my_lim ? mrow[static_cast<int64_t>(t) * a.mst] != 0 : false;
     const bool more = it + 1 < ntiles;
-    if (more) ld.issue(kb16, kst16, (it + 1) * TILE_N, a.T, lds + ((it + 1) & 1) * TILE_BYTES);
-    const char* tile = lds + (it & 1) * TILE_BYTES;
+    if (more) ld.issue(kb16, kst16, (it + 1) * TILE_N, a.T, lds + (1 - slot) * TILE_BYTES);
+    const char* tile = lds + slot * TILE_BYTES;
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
     if (nblk > 0) {
@@ -243,7 +252,14 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
     }
     if (more) wait_vm_lgkm0<0>();
     __syncthreads();
+  };
+  static_assert(RING == 2, "the tile loop is unrolled over the two ring slots");
+  int it = 0;
+  for (; it + 1 < ntiles; it += 2) {
+    tile_step(it, std::integral_constant<int, 0>{});
+    tile_step(it + 1, std::integral_constant<int, 1>{});
   }
+  if (it < ntiles) tile_step(it, std::integral_constant<int, 0>{});
 
   if (active) {
     const int64_t row = static_cast<int64_t>(b) * a.S + s;
