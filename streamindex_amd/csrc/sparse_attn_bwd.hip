@@ -525,7 +525,7 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
   // Each thread moves 2 x 16 bytes of a tile's coefficient block.  The blocks
   // are fetched two tiles ahead into two alternating register sets, so the
   // wait before a block's LDS store leaves the previous and the current
-  // tile's row stores (18 + 18 per thread) in flight.
+  // tile's row stores (10 + 10 per thread at D = 576) in flight.
   u32x4 c0[2], c1[2];
   auto coef_load = [&](int t, u32x4 (&dst)[2]) {
     const u32x4* src = reinterpret_cast<const u32x4*>(coef_row + static_cast<int64_t>(t) * kCoefTile);
@@ -592,6 +592,7 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
       }
     };
     if (DS::MBT % 4 == 0 || wave * MBW < DS::MBT) a_read(std::integral_constant<int, 0>{});
+    uint2 pend[2];  // packed rows of an even block, stored with the next block
     auto block = [&](auto JC) {
       constexpr int j = decltype(JC)::value;
       lds_wait_n<0>();
@@ -617,12 +618,38 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
         // slot of the padded tile is written: a masked or padding slot has
         // P = dS = 0 and no key, so the reduction never reads its row, and
         // unconditional stores keep the prefetch waits exact.
+        uint2 w[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          uint2 w;
-          w.x = pack2<F16>(acc[nb][0], acc[nb][1]);
-          w.y = pack2<F16>(acc[nb][2], acc[nb][3]);
-          *reinterpret_cast<uint2*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + mbi * 16 + 4 * g) = w;
+          w[nb].x = pack2<F16>(acc[nb][0], acc[nb][1]);
+          w[nb].y = pack2<F16>(acc[nb][2], acc[nb][3]);
+        }
+        if constexpr (j % 2 == 0 && j + 1 < MBW) {
+          // held until block j+1 (the next 16 dimensions of the same keys)
+          pend[0] = w[0];
+          pend[1] = w[1];
+        } else if constexpr (j % 2 == 1) {
+          // Blocks j-1 and j regrouped so that lane group g holds 16 bytes:
+          // dimensions 16 mbi(j-1) + 8g + 0..7 of its key (a permlane32 swap
+          // pairs the blocks' lane halves, a permlane16 swap the lane groups);
+          // each store then writes 64 contiguous bytes of 16 keys.
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const auto sx = __builtin_amdgcn_permlane32_swap(pend[nb].x, w[nb].x, false, false);
+            const auto sy = __builtin_amdgcn_permlane32_swap(pend[nb].y, w[nb].y, false, false);
+            const auto tx = __builtin_amdgcn_permlane16_swap(sx[0], sx[1], false, false);
+            const auto ty = __builtin_amdgcn_permlane16_swap(sy[0], sy[1], false, false);
+            u32x4 v;
+            v[0] = tx[0];
+            v[1] = ty[0];
+            v[2] = tx[1];
+            v[3] = ty[1];
+            *reinterpret_cast<u32x4*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + (mbi - 1) * 16 + 8 * g) = v;
+          }
+        } else {
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+            *reinterpret_cast<uint2*>(a.prow + (prow_base + t * kAttnTK + nb * 16 + i16) * D + mbi * 16 + 4 * g) = w[nb];
         }
       }
     };
