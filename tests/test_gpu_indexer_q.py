@@ -8,7 +8,8 @@ and the GPU result goes through the same gate as the bf16 indexer
 wherever the k-th gap exceeds 1e-4 of the row scale, recall >= 0.999).
 Shapes: the reference tests' ragged ones (S=47, T=73), causal ratio 4 and an
 explicit mask, rows with no legal key, H_I = 16 / 40 / 64, top_k up to
-1024, and the quantising wrapper on bf16 inputs.
+1024, rows long enough to compact the selection buffer several times, and the
+quantising wrapper on bf16 inputs.
 """
 
 import numpy as np
@@ -85,6 +86,18 @@ def test_large_topk_sampled_rows(cuda_device):
     rows = np.random.default_rng(0).choice(S, 96, replace=False)
     rows[:3] = [0, 2, S - 1]   # no legal key, no legal key, full row
     _check(q4, qs, k8, ks, w, 1024, idx, sc, ratio=4, rows=rows, label="q-1024")
+
+
+@pytest.mark.parametrize("top_k", [512, 640])
+def test_compacting_rows(cuda_device, top_k):
+    # top_k in (192, 640] runs the 1152-key selection buffer; rows of up to
+    # 4096 keys compact it several times (first past 1024 held keys)
+    B, S, T, H = 1, 8192, 4096, 64
+    _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 31 + top_k)
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, top_k, causal_ratio=2)
+    rows = np.random.default_rng(top_k).choice(S, 40, replace=False)
+    rows[:3] = [S - 1, S - 2, 2 * top_k]   # the longest rows, and one just past top_k legal keys
+    _check(q4, qs, k8, ks, w, top_k, idx, sc, ratio=2, rows=rows, label=f"q-compact-{top_k}")
 
 
 def test_quantising_wrapper_and_validation(cuda_device):
