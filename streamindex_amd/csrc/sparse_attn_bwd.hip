@@ -593,6 +593,7 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
     };
     if (DS::MBT % 4 == 0 || wave * MBW < DS::MBT) a_read(std::integral_constant<int, 0>{});
     uint2 pend[2];  // packed rows of an even block, stored with the next block
+    static_assert(DS::MBT % 4 == 0 || MBW == 1, "both blocks of a stored pair are inside the row");
     auto block = [&](auto JC) {
       constexpr int j = decltype(JC)::value;
       lds_wait_n<0>();
