@@ -117,7 +117,8 @@ def sparse_attn_fwd(
 
 
 # Default cap on the backward's workspace: at most this, and at most a quarter
-# of the device memory free at the call.
+# of the device memory free at the call (the driver's free memory plus what
+# the caching allocator holds unused).
 BWD_WORKSPACE_CAP = 8 << 30
 
 
@@ -143,8 +144,9 @@ def sparse_attn_bwd(
 
     Returns ``(dq, dkv, dattn_sink)`` shaped and typed like ``q``, ``kv`` and
     ``attn_sink``.  ``workspace_bytes`` caps the scratch memory (default:
-    ``BWD_WORKSPACE_CAP`` or a quarter of the free device memory, whichever is
-    smaller); the query rows are processed in as few chunks as fit it.
+    ``BWD_WORKSPACE_CAP`` or a quarter of the free device memory, cached
+    blocks included, whichever is smaller); the query rows are processed in as
+    few chunks as fit it.
     ``row_len`` as in :func:`sparse_attn_fwd` (an extension): columns at or
     past it are masked and their tiles skipped.
     """
@@ -184,8 +186,13 @@ def sparse_attn_bwd(
     L = _lib.load()
     with torch.cuda.device(q.device):
         if workspace_bytes is None:
+            # Memory the caching allocator holds but has not handed out counts
+            # as free too: the driver's free figure alone moves with every
+            # segment the allocator maps, and with it the workspace size,
+            # which then misses the cached block and allocates anew.
             free, _ = torch.cuda.mem_get_info(q.device)
-            workspace_bytes = min(BWD_WORKSPACE_CAP, free // 4)
+            cached = torch.cuda.memory_reserved(q.device) - torch.cuda.memory_allocated(q.device)
+            workspace_bytes = min(BWD_WORKSPACE_CAP, (free + cached) // 4)
         need = L.si_sparse_attn_bwd_workspace_bytes(B, S, H, D, N_kv, K, int(workspace_bytes))
         if need < 0:
             raise ValueError(L.si_last_error().decode("utf-8", "replace"))
