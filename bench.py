@@ -785,7 +785,7 @@ def main():
 
     if not args.no_attn:
         say("sparse attention config[3] on config[1]'s indexer output")
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1, idx=c1_idx, bwd=not args.no_attn_bwd,
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, 10, 5, idx=c1_idx, bwd=not args.no_attn_bwd,
                              parity_rows=64)
         c3 = {"indices": "config[1] chunked_indexer_topk output (int64, -1 past the causal count)",
               "ms": ra["ms"], "tflops": ra["flops"] / (ra["ms"] * 1e-3) / 1e12,
@@ -801,7 +801,7 @@ def main():
         del ra
         torch.cuda.empty_cache()
         say("sparse attention on random causal indices (secondary)")
-        rr = run_sparse_attn(65536, 16384, 64, 576, 512, 3, 1)
+        rr = run_sparse_attn(65536, 16384, 64, 576, 512, 10, 5)
         extra["sparse_attn_random_idx"] = {"ms": rr["ms"], "tflops": rr["flops"] / (rr["ms"] * 1e-3) / 1e12,
                                            "unique_gbps": rr["unique_bytes"] / (rr["ms"] * 1e-3) / 1e9}
         del rr
@@ -828,20 +828,20 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_indexer_q:
         say("fp4/fp8 indexer S=64K and S=1M")
-        extra["indexer_q_s64k"] = run_indexer_q(65536, args.ratio, args.top_k, 5, 1)
+        extra["indexer_q_s64k"] = run_indexer_q(65536, args.ratio, args.top_k, 10, 5)
         if not args.no_long:
             extra["indexer_q_s1m"] = run_indexer_q(1 << 20, args.ratio, args.top_k, 1, 1, parity_rows=64)
         torch.cuda.empty_cache()
 
     if not args.no_e2e:
         say("end-to-end CSA forward S=64K")
-        extra["csa_e2e_s64k"] = run_csa_e2e(65536, 3, 1, 256, bwd=not args.no_attn_bwd)
+        extra["csa_e2e_s64k"] = run_csa_e2e(65536, 5, 3, 256, bwd=not args.no_attn_bwd)
         say("end-to-end CSA forward S=1M (config[4])")
         extra["csa_e2e_s1m"] = run_csa_e2e(1 << 20, 1, 1, args.e2e_parity_rows)
         say("end-to-end CSA forward S=1M with the fp4/fp8 indexer")
         extra["csa_e2e_s1m_quantized_indexer"] = run_csa_e2e(1 << 20, 1, 1, 256, quantized=True)
         say("end-to-end HCA forward S=64K")
-        extra["hca_e2e_s64k"] = run_hca_e2e(65536, 3, 1, 8, bwd=not args.no_attn_bwd)
+        extra["hca_e2e_s64k"] = run_hca_e2e(65536, 10, 3, 8, bwd=not args.no_attn_bwd)
     torch.cuda.empty_cache()
 
     counters = None
