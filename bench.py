@@ -179,12 +179,13 @@ def run_indexer(S, ratio, top_k, chunk_s, chunk_t, steps, warmup, H=64, D=128, s
     q, k, w = synth.indexer_inputs(1, S, H, D, ratio=ratio, seed=seed, device=dev)
     T = k.shape[1]
     fn = lambda: chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=chunk_s, chunk_t=chunk_t)  # noqa: E731
+    # (the peak-memory probe empties the allocator cache and idles the GPU, so
+    # it runs before the warm-up: the timed calls follow the warm-up directly)
+    peak = _peak_gib(fn)
     for _ in range(max(1, warmup)):
         out = fn()
     torch.cuda.synchronize()
-    peak = _peak_gib(fn)
     stream = torch.cuda.current_stream(dev)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     ms = _events_time(fn, steps, stream)
     wall = (time.perf_counter() - t0) * 1e3 / steps
@@ -203,9 +204,9 @@ def run_indexer_sweep(q, k, w, ratio, top_ks, steps):
     out = {}
     for kk in top_ks:
         fn = lambda: chunked_indexer_topk(q, k, w, kk, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)  # noqa: E731
+        peak = _peak_gib(fn)
         fn()
         torch.cuda.synchronize()
-        peak = _peak_gib(fn)
         ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
         out[str(kk)] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
                         "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "peak_hbm_gib": peak}
@@ -544,10 +545,10 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     q, kv, kvc, sink = synth.csa_attn_inputs(1, S, n_h, d, S // m, seed=2027, device=dev)
     fn = lambda: flash_csa_forward(q, kv, kvc, qi, ki, w, sink, n_win=n_win, top_k=top_k, m=m,  # noqa: E731
                                    quantized_indexer=quantized)
+    peak = _peak_gib(fn)
     for _ in range(max(1, warmup)):
         fn()
     torch.cuda.synchronize()
-    peak = _peak_gib(fn)
     stream = torch.cuda.current_stream(dev)
     ms = _events_time(fn, steps, stream)
     # stage split of one call (same three steps flash_csa_forward runs)
