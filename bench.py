@@ -50,6 +50,7 @@ from streamindex_amd import (build_hca_topk_idxs, chunked_indexer_topk, csa_topk
                              flash_csa_forward, flash_hca_forward, sparse_attn, sparse_attn_bwd, sparse_attn_fwd)
 from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
+from streamindex_amd import sparse_attn as sparse_attn_mod  # noqa: E402
 from streamindex_amd.csa import csa_row_len  # noqa: E402
 from streamindex_amd.hca import hca_row_len  # noqa: E402
 
@@ -64,6 +65,8 @@ REF_H200_GIB = {65536: 0.59, 262144: 1.71, 1048576: 6.21}
 REF_H200_TOPK_S256K_MS = {64: 1754, 256: 1881, 512: 1934, 1024: 1996, 2048: 2217}
 # V4-Pro point, top_k=1024 at S=1M: RESULTS.md:86-96 (ms, GiB)
 REF_H200_S1M_K1024 = (31973.3, 12.27)
+# Backward workspace caps timed at config[3] (GiB)
+BWD_SWEEP_GIB = (1, 2, 4, 8)
 
 
 
@@ -245,10 +248,12 @@ def run_c2(ratio, steps):
 # One pass per counter group (rocprofv3 does not split counters over passes):
 # the MFMA pass stays within 8 SQ and 2 GRBM counters, FETCH_SIZE takes 3 of
 # the 4 TCC counters and WRITE_SIZE 2, so they run separately.
+# The MFMA pass also runs the S = 1M indexer (the north-star shape); the byte
+# passes do not need it.
 COUNTER_PASSES = (
-    ("mfma", ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "GRBM_GUI_ACTIVE", "GRBM_COUNT")),
-    ("fetch", ("FETCH_SIZE",)),
-    ("write", ("WRITE_SIZE",)),
+    ("mfma", ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "GRBM_GUI_ACTIVE", "GRBM_COUNT"), True),
+    ("fetch", ("FETCH_SIZE",), False),
+    ("write", ("WRITE_SIZE",), False),
 )
 N_SIMD = 1024           # 256 CUs x 4 SIMDs
 N_XCD = 8               # GRBM_GUI_ACTIVE is summed over the XCDs
@@ -256,11 +261,23 @@ MFMA_FLOP = 32 * 32 * 16 * 2   # v_mfma_f32_32x32x16_bf16
 COPY_MIB = 1024         # plain device copy used to scale the byte counters
 
 
-def counter_child(ratio=4, top_k=512):
-    """The workload the counter passes profile: config[1]'s indexer (1 warm-up
-    + 3 launches), sparse attention at config[3] on its output (1 + 2), and a
+S1M = 1 << 20
+
+
+def counter_child(ratio=4, top_k=512, s1m=False):
+    """The workload the counter passes profile: with `s1m` first the S = 1M
+    indexer (1 warm-up + 2 launches), then config[1]'s indexer (1 warm-up + 3
+    launches), sparse attention at config[3] on its output (1 + 2), and a
     plain 1 GiB device copy (x3) that calibrates the byte counters."""
     dev = torch.device("cuda:0")
+    if s1m:
+        q, k, w = synth.indexer_inputs(1, S1M, 64, 128, ratio=ratio, seed=2026, device=dev)
+        for _ in range(3):
+            idx, sc = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)
+            del idx, sc
+        torch.cuda.synchronize()
+        del q, k, w
+        torch.cuda.empty_cache()
     q, k, w = synth.indexer_inputs(1, 65536, 64, 128, ratio=ratio, seed=2026, device=dev)
     for _ in range(4):
         idx, _ = chunked_indexer_topk(q, k, w, top_k, causal_ratio=ratio, chunk_s=2048, chunk_t=8192)
@@ -297,6 +314,33 @@ def _pick(disp, name, last):
     return rows[-last:]
 
 
+def _pick_first(disp, name, skip, count):
+    rows = [v for _, v in sorted(disp.items()) if name in v["kernel"]]
+    return rows[skip:skip + count]
+
+
+def _mfma_summary(rows, flops):
+    """Clock, MFMA-busy fraction and counter-derived utilisation of dispatches
+    from the MFMA pass (busy cycles over 1,024 SIMDs; GRBM_GUI_ACTIVE summed
+    over 8 XCDs)."""
+    ns = float(np.mean([v["ns"] for v in rows]))
+    cyc = float(np.mean([v["GRBM_GUI_ACTIVE"] for v in rows])) / N_XCD
+    busy = float(np.mean([v["SQ_VALU_MFMA_BUSY_CYCLES"] for v in rows]))
+    insts = float(np.mean([v["SQ_INSTS_MFMA"] for v in rows]))
+    return {
+        "kernel": rows[0]["kernel"].split("(")[0],
+        "dispatches": len(rows), "avg_ms": ns * 1e-6,
+        "clock_ghz": cyc / ns,
+        "mfma_busy_pct": 100.0 * busy / N_SIMD / cyc,
+        "mfma_insts": insts,
+        "executed_mfma_flops": insts * MFMA_FLOP,
+        "algorithmic_flops": flops,
+        "mfma_util_pct_from_counters": 100.0 * insts * MFMA_FLOP / (ns * 1e-9) / 1e12 / PEAK_BF16_TFLOPS,
+        "mfma_util_pct_from_time": 100.0 * flops / (ns * 1e-9) / 1e12 / PEAK_BF16_TFLOPS,
+        "valu_per_mfma": float(np.mean([v["SQ_INSTS_VALU"] for v in rows])) / max(insts, 1.0),
+    }
+
+
 def run_counters(timeout=240):
     """Runs the counter passes over `counter_child` under rocprofv3 and returns
     the indexer's MFMA-busy fraction, shader clock and counter-derived MFMA
@@ -314,10 +358,10 @@ def run_counters(timeout=240):
     tmp = tempfile.mkdtemp(prefix="si_pmc_", dir="/tmp")
     env = dict(os.environ, TMPDIR="/tmp")
     passes = {}
-    for name, ctrs in COUNTER_PASSES:
+    for name, ctrs, s1m in COUNTER_PASSES:
         d = os.path.join(tmp, name)
         cmd = [prof, "--pmc", *ctrs, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
-               sys.executable, os.path.abspath(__file__), "--counter-child"]
+               sys.executable, os.path.abspath(__file__), "--counter-child"] + (["--counter-s1m"] if s1m else [])
         print(f"[bench] counter pass {name}: {' '.join(ctrs)}", file=sys.stderr, flush=True)
         p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                              start_new_session=True)
@@ -332,25 +376,18 @@ def run_counters(timeout=240):
             return {"error": f"counter pass {name}: no counter file (rc {p.returncode})",
                     "log_tail": log.decode("utf-8", "replace")[-600:]}
         passes[name] = _read_counters(files[0])
-    res = {"passes": [" ".join(c) for _, c in COUNTER_PASSES], "cmd": "rocprofv3 --pmc <pass> --output-format csv -- "
-           "python3 bench.py --counter-child"}
-    idx = _pick(passes["mfma"], "indexer_topk_kernel", 3)
+    res = {"passes": [" ".join(c) for _, c, _ in COUNTER_PASSES],
+           "cmd": "rocprofv3 --pmc <pass> --output-format csv -- python3 bench.py --counter-child "
+                  "[--counter-s1m: MFMA pass]"}
+    # The S = 1M launches come first in the MFMA pass: the first three
+    # indexer dispatches, of which the first is the warm-up.  config[1]'s are
+    # the last three (after its own warm-up).
+    s1m = _pick_first(passes["mfma"], "indexer_topk", 1, 2)
+    if len(s1m) == 2:
+        res["indexer_s1m"] = _mfma_summary(s1m, synth.indexer_flops(S1M, S1M // 4, 64, 128, 4))
+    idx = _pick(passes["mfma"], "indexer_topk", 3)
     if idx:
-        ns = float(np.mean([v["ns"] for v in idx]))
-        cyc = float(np.mean([v["GRBM_GUI_ACTIVE"] for v in idx])) / N_XCD
-        busy = float(np.mean([v["SQ_VALU_MFMA_BUSY_CYCLES"] for v in idx]))
-        insts = float(np.mean([v["SQ_INSTS_MFMA"] for v in idx]))
-        flops = synth.indexer_flops(65536, 16384, 64, 128, 4)
-        res["indexer_c1"] = {
-            "dispatches": len(idx), "avg_ms": ns * 1e-6,
-            "clock_ghz": cyc / ns,
-            "mfma_busy_pct": 100.0 * busy / N_SIMD / cyc,
-            "mfma_insts": insts,
-            "executed_mfma_flops": insts * MFMA_FLOP,
-            "algorithmic_flops": flops,
-            "mfma_util_pct_from_counters": 100.0 * insts * MFMA_FLOP / (ns * 1e-9) / 1e12 / PEAK_BF16_TFLOPS,
-            "valu_per_mfma": float(np.mean([v["SQ_INSTS_VALU"] for v in idx])) / max(insts, 1.0),
-        }
+        res["indexer_c1"] = _mfma_summary(idx, synth.indexer_flops(65536, 16384, 64, 128, 4))
     copies = _pick(passes["fetch"], "copyBuffer", 3)
     wcopies = _pick(passes["write"], "copyBuffer", 3)
     if copies and wcopies:
@@ -358,7 +395,7 @@ def run_counters(timeout=240):
         fscale = nbytes / (float(np.mean([v["FETCH_SIZE"] for v in copies])) * 1024.0)
         wscale = nbytes / (float(np.mean([v["WRITE_SIZE"] for v in wcopies])) * 1024.0)
         res["fetch_scale"], res["write_scale"] = fscale, wscale
-        for key, kname, last in (("indexer_c1", "indexer_topk_kernel", 3), ("sparse_attn_c3", "sparse_attn_fwd_kernel", 2)):
+        for key, kname, last in (("indexer_c1", "indexer_topk", 3), ("sparse_attn_c3", "sparse_attn_fwd_kernel", 2)):
             f = _pick(passes["fetch"], kname, last)
             wr = _pick(passes["write"], kname, last)
             if f and wr:
@@ -457,16 +494,25 @@ def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=T
         g = torch.Generator(device=dev)
         g.manual_seed(2028)
         do = torch.randn(q.shape, generator=g, device=dev, dtype=torch.bfloat16).mul_(0.5)
-        bfn = lambda: sparse_attn_bwd(q, kv, sink, idx, o, lse, do, D ** -0.5)  # noqa: E731
-        torch.cuda.reset_peak_memory_stats(dev)
-        base = torch.cuda.memory_allocated(dev)
+        def bfn(cap=None):
+            return sparse_attn_bwd(q, kv, sink, idx, o, lse, do, D ** -0.5, workspace_bytes=cap)
+
         for _ in range(max(1, warmup)):
-            grads = bfn()
-        del grads
+            bfn()  # (each call's gradients are freed before the next call)
         torch.cuda.synchronize()
         res["bwd_ms"] = _events_time(bfn, steps, stream)
         res["bwd_flops"] = 10.0 * H * D * nvalid
-        res["bwd_peak_extra_gib"] = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+        # memory one call adds beyond its inputs: dq, dkv, dsink and the workspace
+        res["bwd_peak_extra_gib"] = _peak_gib(bfn)
+        res["bwd_workspace_cap_gib"] = sparse_attn_mod.BWD_WORKSPACE_CAP / 2 ** 30
+        sweep = []
+        for cap_gib in BWD_SWEEP_GIB:
+            f = lambda: bfn(cap_gib << 30)  # noqa: E731
+            f()
+            torch.cuda.synchronize()
+            sweep.append({"workspace_cap_gib": cap_gib, "ms": _events_time(f, max(3, steps // 2), stream),
+                          "peak_extra_gib": _peak_gib(f)})
+        res["bwd_workspace_sweep"] = sweep
         res["bwd_parity"] = attn_bwd_check(q, kv, sink, idx, o, lse, do, bfn())
     return res
 
@@ -682,6 +728,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (config[0] on the host)")
     ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--counter-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--counter-s1m", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--only-indexer", action="store_true", help="indexer timing only (for profilers)")
     ap.add_argument("--only-attn", action="store_true",
                     help="config[3] sparse-attention timing only, on config[1]'s indexer output (for profilers)")
@@ -703,7 +750,7 @@ def main():
                     help="run 5 plain device copies of MIB MiB (scales HBM byte counters) and exit")
     args = ap.parse_args()
     if args.counter_child:
-        counter_child(args.ratio, args.top_k)
+        counter_child(args.ratio, args.top_k, s1m=args.counter_s1m)
         return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
@@ -797,7 +844,9 @@ def main():
         if "bwd_ms" in ra:
             c3["bwd"] = {"ms": ra["bwd_ms"], "tflops": ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12,
                          "mfma_frac": ra["bwd_flops"] / (ra["bwd_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                         "peak_extra_gib": ra["bwd_peak_extra_gib"], "parity": ra["bwd_parity"]}
+                         "peak_extra_gib": ra["bwd_peak_extra_gib"],
+                         "default_workspace_cap_gib": ra["bwd_workspace_cap_gib"],
+                         "workspace_sweep": ra["bwd_workspace_sweep"], "parity": ra["bwd_parity"]}
         extra["sparse_attn_c3"] = c3
         del ra
         torch.cuda.empty_cache()

@@ -63,8 +63,10 @@ size_t si_indexer_topk_workspace_bytes(int64_t B, int64_t S, int64_t T, int64_t 
  *                     Must be 0 when mask != NULL.
  *   out_idx    [B,S,top_k] int64, contiguous: best-first, -1 past the legal count
  *   out_scores [B,S,top_k] fp32,  contiguous: best-first, -inf past the legal count
- * Ties rank the smaller key index first.  Supported: D in {32,64,128} with
- * H <= 128, D = 256 with H <= 64 and top_k <= 1536; 1 <= top_k <= 2048.
+ * Ties rank the smaller key index first.  Supported: D in {32,64,128,256},
+ * 1 <= H <= 256, 1 <= top_k <= 4096 (the reference takes any power-of-two
+ * H >= 16 and D, flash_sparse/triton/indexer_score.py:145-150, and any
+ * top_k, chunked_indexer.py:47-57).
  */
 int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, const int64_t* k_strides,
                     const void* weights, int w_dtype, const int64_t* w_strides, const uint8_t* mask,
@@ -89,6 +91,21 @@ int si_indexer_topk(const void* q, const int64_t* q_strides, const void* k_idx, 
 int si_indexer_set_topk_kernel(int mode);
 
 /*
+ * The kernel si_indexer_topk would launch for a shape under the current
+ * si_indexer_set_topk_kernel mode, without launching anything.  *kernel
+ * receives 1 (one query row per wave, two workgroups per CU where registers
+ * allow: H <= 128, or 64 at D = 256, and top_k <= 2048, or 1536 at D = 256),
+ * 2 (four 32-head blocks per wave: D = 128, T >= 64, top_k <= 1152) or 3
+ * (each row's heads split over two or four waves: the other shapes up to
+ * H = 256 and top_k = 4096); *capacity the selection buffer's keys per row.
+ * Either pointer may be NULL.  Returns a status code (SI_ERR_UNSUPPORTED
+ * for a shape no kernel serves).  No counterpart in the reference: a
+ * planning query for tests and tuning.
+ */
+int si_indexer_topk_plan(int64_t S, int64_t T, int64_t H, int64_t D, int64_t top_k, int64_t causal_ratio,
+                         int32_t* kernel, int32_t* capacity);
+
+/*
  * Materialised indexer score matrix scores[b,s,t] = sum_h w[b,s,h]*relu(q[b,s,h,:].k[b,t,:]),
  * fp32 with strides score_strides[3].  No mask.
  * Replaces flash_sparse/triton/indexer_score.py:41-179 (_indexer_score_kernel, indexer_score).
@@ -107,7 +124,7 @@ int si_indexer_score(const void* q, const int64_t* q_strides, const void* k_idx,
  *   topk_idxs [B,S,K] int32 (idx_is_i64 = 0) or int64 (1); -1 or >= N_kv = masked.
  *   o [B,S,H,D] out, q's type; lse [B,S,H] fp32 out (natural log, sink included).
  *   P is rounded to the element type before P.V, as the reference does.
- * Supported: H <= 128, D in {32,64,128,256,512,576}.
+ * Supported: any H (64-head groups), D in {32,64,128,256,512,576}.
  */
 int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
                        const float* attn_sink, const void* topk_idxs, int idx_is_i64,

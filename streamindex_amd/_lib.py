@@ -35,6 +35,7 @@ SIGNATURES = {
     "si_last_error": (ctypes.c_char_p, []),
     "si_indexer_topk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "si_indexer_set_topk_kernel": (_I32, [_I32]),
+    "si_indexer_topk_plan": (_I32, [_I64, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "si_indexer_topk": (_I32, [_P, _I64P, _P, _I64P, _P, _I32, _I64P, _P, _I64P,
                                _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "si_indexer_score": (_I32, [_P, _I64P, _P, _I64P, _P, _I32, _I64P,

@@ -49,7 +49,8 @@ COMMON_FLAGS = [
 EXTRA_FLAGS = {
     "sparse_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     **{f"indexer_inst_{u}.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-       for u in ("d32", "d32_wide", "d64", "d64_wide", "d128", "d128_wide", "d256")},
+       for u in ("d32", "d32_wide", "d64", "d64_wide", "d128", "d128_wide", "d256",
+                 "split_d32", "split_d64", "split_d128", "split_d256")},
 }
 
 

@@ -39,7 +39,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .indexer import _check_common, _prep, MAX_TOPK
+from .indexer import _check_common, _prep, MAX_HEADS_Q, MAX_TOPK, MAX_TOPK_Q
 from .sparse_attn import sparse_attn
 
 __all__ = ["flash_csa_forward", "build_csa_topk_idxs", "csa_topk_idxs", "build_sliding_window_idxs", "csa_row_len"]
@@ -92,8 +92,8 @@ def csa_topk_idxs(q_idx: torch.Tensor, k_idx_compressed: torch.Tensor, indexer_w
     scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q_idx.device) if return_scores else None
     L = _lib.load()
     if quantized:
-        if D_I != 128 or H_I > 64:
-            raise ValueError("the quantised indexer needs D_I = 128 and H_I <= 64")
+        if D_I != 128 or H_I > MAX_HEADS_Q or top_k > MAX_TOPK_Q:
+            raise ValueError(f"the quantised indexer needs D_I = 128, H_I <= {MAX_HEADS_Q} and top_k <= {MAX_TOPK_Q}")
         from .quant import act_quant, fp4_act_quant
 
         q4, qs = fp4_act_quant(q_idx, 32)

@@ -17,7 +17,7 @@ int set_error(int code, const std::string& msg) {
 extern "C" const char* si_last_error(void) { return si::g_last_error.c_str(); }
 
 // Bumped whenever an entry point's signature or semantics change.
-extern "C" int si_abi_version(void) { return 7; }
+extern "C" int si_abi_version(void) { return 8; }
 
 // The fused indexer keeps every selection buffer in LDS, so the top-k entry
 // needs no device workspace at any size.  Kept so callers that size a

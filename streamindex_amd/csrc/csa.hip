@@ -104,6 +104,7 @@ __global__ __launch_bounds__(256) void hca_idx_kernel(HcaIdxArgs a) {
 
 template <int C>
 static int launch_score_topk(const ScoreTopkArgs& a, hipStream_t st) {
+  if (a.top_k > WaveSelect<C>::MAX_TOPK) return set_error(SI_ERR_UNSUPPORTED, "top_k exceeds the selection capacity");
   const int64_t rows = static_cast<int64_t>(a.B) * a.S;
   const int64_t nblk = (rows + 3) / 4;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
@@ -123,7 +124,7 @@ extern "C" int si_csa_scores_topk(const float* scores, const int64_t* score_stri
   if (B < 0 || S < 0 || T < 0) return set_error(SI_ERR_INVALID, "negative dimension");
   if (B > 0x7fffffff || S > 0x7fffffff || T > 0x7fffffff) return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
   if (top_k <= 0) return set_error(SI_ERR_INVALID, "top_k must be positive");
-  if (top_k > 2048) return set_error(SI_ERR_UNSUPPORTED, "top_k > 2048 is not supported");
+  if (top_k > 4096) return set_error(SI_ERR_UNSUPPORTED, "top_k > 4096 is not supported");
   if (causal_ratio < 0 || causal_ratio > 0x7fffffff) return set_error(SI_ERR_INVALID, "bad causal_ratio");
   if (n_win < 0 || n_win > 0x7fffffff) return set_error(SI_ERR_INVALID, "n_win must be non-negative");
   if (idx_offset < 0 || idx_offset + T > 0x7fffffff)
@@ -147,7 +148,8 @@ extern "C" int si_csa_scores_topk(const float* scores, const int64_t* score_stri
   if (a.top_k <= 192) return launch_score_topk<512>(a, st);
   if (a.top_k <= 640) return launch_score_topk<1024>(a, st);
   if (a.top_k <= 1536) return launch_score_topk<2048>(a, st);
-  return launch_score_topk<4096>(a, st);
+  if (a.top_k <= 2048) return launch_score_topk<4096>(a, st);
+  return launch_score_topk<4608>(a, st);
 }
 
 extern "C" int si_hca_topk_idxs(int64_t B, int64_t S, int64_t n_win, int64_t n_compressed, int64_t m_prime,

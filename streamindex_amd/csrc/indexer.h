@@ -32,6 +32,7 @@ struct IndexerArgs {
   int idx_offset;
   float* scores;        // score kernel: [B,S,T]
   int64_t ssb, sss, sst;
+  int accumulate;       // score kernel: add to the scores already stored (a later head group)
 };
 
 // Selection-buffer capacities the top-k kernel is instantiated for: 256,
@@ -63,7 +64,11 @@ extern int g_topk_kernel_mode;
 // (its single wave per SIMD pays per-row costs -- final sort, compactions,
 // workgroup tail -- that the two-workgroup-per-CU indexer_topk_kernel
 // hides, and wins in the MFMA loop that long rows spend their time in).
+// It needs T >= 64: the copies of a tile past the last one re-read rows 0..63
+// of k_idx (at any mode; SI_TOPK_KERNEL_WIDE then falls back to the other
+// kernel).
 inline bool topk_wide_preferred(const IndexerArgs& a) {
+  if (a.T < 64) return false;
   if (g_topk_kernel_mode == 1) return false;
   if (g_topk_kernel_mode == 2) return true;
   if (a.H > 96) return true;
@@ -73,5 +78,20 @@ inline bool topk_wide_preferred(const IndexerArgs& a) {
 
 template <int HB, int D>
 int launch_score(const IndexerArgs& a, hipStream_t st);
+
+// Head-split top-k kernel (indexer_topk_split.h): HS waves per query row,
+// HBH 32-head blocks per wave, selection capacity C.
+template <int HS, int HBH, int D, int C>
+int launch_topk_split(const IndexerArgs& a, hipStream_t st);
+
+// Which top-k kernel serves a shape, and with which selection capacity
+// (the C-ABI dispatch and si_indexer_topk_plan both read it).
+enum TopkKernel { TOPK_NARROW = 1, TOPK_WIDE = 2, TOPK_SPLIT = 3 };
+struct TopkPlan {
+  int kernel;  // TopkKernel
+  int cap;     // selection capacity (keys per row)
+  int hb;      // 32-head blocks per wave (narrow / wide: of the whole row)
+  int hs;      // waves per query row (split kernel), else 1
+};
 
 }  // namespace si

@@ -437,7 +437,7 @@ void indexer_topk_kernel(IndexerArgs a) {
         // groups: when both waves of a SIMD are in their MFMA sections, the
         // one further along issues first, so the two drift apart instead of
         // interleaving and reaching their loop tops together.
-        __builtin_amdgcn_s_setprio(ph);
+        __builtin_amdgcn_s_setprio(ph < 3 ? ph : 3);  // (the priority field is 2 bits wide)
         const float e = qfr.epilogue(acc[eg], emb);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -572,7 +572,10 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int t = tbase + nb * 32 + (lane & 31);
-        if (nb < nblk && lane < 32 && t < a.T) orow[static_cast<int64_t>(t) * a.sst] = sc[nb];
+        if (nb < nblk && lane < 32 && t < a.T) {
+          float* o = orow + static_cast<int64_t>(t) * a.sst;
+          *o = a.accumulate ? *o + sc[nb] : sc[nb];
+        }
       }
     }
     tile_barrier();

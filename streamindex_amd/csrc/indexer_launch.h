@@ -18,6 +18,7 @@ int launch_topk(const IndexerArgs& a, hipStream_t st) {
   if constexpr (!topk_fits_lds<HB, D, C>()) {
     return set_error(SI_ERR_UNSUPPORTED, "top_k too large for this head dim (the selection buffers exceed LDS)");
   } else {
+  if (a.top_k > WaveSelect<C>::MAX_TOPK) return set_error(SI_ERR_UNSUPPORTED, "top_k exceeds the selection capacity");
   constexpr int NW = TopkShape<C>::NW;
   const int nqb = (a.S + NW - 1) / NW;
   const int64_t nblk = static_cast<int64_t>(nqb) * a.B;

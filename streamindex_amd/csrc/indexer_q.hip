@@ -278,6 +278,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
 
 template <int HB, int D, int C>
 static int launch_q(const IndexerQArgs& a, hipStream_t st) {
+  if (a.top_k > WaveSelect<C>::MAX_TOPK) return set_error(SI_ERR_UNSUPPORTED, "top_k exceeds the selection capacity");
   constexpr int NW = TopkShape<C>::NW;
   const int64_t nqb = (static_cast<int64_t>(a.S) + NW - 1) / NW;
   const int64_t grid = nqb * a.B;

@@ -419,6 +419,8 @@ int launch_topk_wide(const IndexerArgs& a, hipStream_t st) {
   if constexpr (!topk_wide_fits<HB, D, C>()) {
     return set_error(SI_ERR_UNSUPPORTED, "shape not served by the four-M-block top-k kernel");
   } else {
+  if (a.top_k > WaveSelect<C>::MAX_TOPK) return set_error(SI_ERR_UNSUPPORTED, "top_k exceeds the selection capacity");
+  if (a.T < 64) return set_error(SI_ERR_UNSUPPORTED, "the four-M-block kernel needs T >= 64");
   constexpr int ROWS = 4 * (4 / HB);
   const int nqb = (a.S + ROWS - 1) / ROWS;
   const int64_t nblk = static_cast<int64_t>(nqb) * a.B;

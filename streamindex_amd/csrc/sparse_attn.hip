@@ -625,7 +625,7 @@ extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides
     return set_error(SI_ERR_INVALID, "null pointer argument");
   if (B > 0x7fffffff || S > 0x7fffffff || N_kv > 0x7fffffff || K > 0x7fffffff)
     return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
-  if (H > 128) return set_error(SI_ERR_UNSUPPORTED, "H > 128 is not supported");
+  if (H > 0x7fffffff) return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
   if (q_strides[3] != 1 || kv_strides[2] != 1 || o_strides[3] != 1)
     return set_error(SI_ERR_INVALID, "q, kv and o need a contiguous last dimension");
   if ((q_strides[0] | q_strides[1] | q_strides[2] | kv_strides[0] | kv_strides[1]) % 8)

@@ -1114,7 +1114,7 @@ extern "C" int si_sparse_attn_bwd_ragged(const void* q, const int64_t* q_strides
   if (!dsink || (B > 0 && N_kv > 0 && !dkv)) return set_error(SI_ERR_INVALID, "null pointer argument");
   if (B * N_kv >= (int64_t{1} << 31) || B * S >= (int64_t{1} << 31) || K > 0x7fffffff)
     return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
-  if (H > 128) return set_error(SI_ERR_UNSUPPORTED, "H > 128 is not supported");
+  if (H > 0x7fffffff) return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
   if (!bwd_supported_d(D))
     return set_error(SI_ERR_UNSUPPORTED,
                      "unsupported head dim D=" + std::to_string(D) + " (supported: 32, 64, 128, 256, 512, 576)");

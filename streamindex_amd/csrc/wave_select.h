@@ -126,8 +126,8 @@ template <int C>
 struct WaveSelect {
   static constexpr int E = C / kWave;   // 64-key rows in the buffer
   static constexpr int CMAX = C - 192;  // most keys a compaction keeps
-  static_assert(C % kWave == 0 && E >= 4 && E <= 64, "capacity must be 64 * E, 4 <= E <= 64");
-  // The final sort holds at most 32 keys per lane: capacities serve top_k <= 2048.
+  // A compaction holds E keys per lane in registers (2E VGPRs).
+  static_assert(C % kWave == 0 && E >= 4 && E <= 72, "capacity must be 64 * E, 4 <= E <= 72");
 
   uint64_t* buf;        // this wave's private LDS buffer, key at position p = buf[p]
   int n;                // keys held (wave-uniform)
@@ -279,9 +279,17 @@ struct WaveSelect {
   static constexpr int SE_CAP = (C - 192) <= 1 * kWave ? 1 : (C - 192) <= 2 * kWave ? 2
                               : (C - 192) <= 4 * kWave ? 4 : (C - 192) <= 8 * kWave ? 8
                               : (C - 192) <= 16 * kWave ? 16 : 32;
+  // Above 2048 keys (32 per lane) finish() sorts two 2048-key runs and merges
+  // them, which needs room for 4096 keys in the buffer.
+  static constexpr bool MERGED = C >= 4096 + 192;
+  // Largest top_k this capacity serves: what a compaction may keep, and what
+  // the final sort writes.  Launchers reject anything larger.
+  static constexpr int MAX_TOPK = MERGED ? (CMAX < 4096 ? CMAX : 4096) : (CMAX < SE_CAP * kWave ? CMAX : SE_CAP * kWave);
 
   __device__ __forceinline__ void finish(const TopkRowOut& out, int lane) {
-    if (top_k <= 1 * kWave) {
+    if (top_k > 32 * kWave) {
+      if constexpr (MERGED) finish_merged(out, lane);
+    } else if (top_k <= 1 * kWave) {
       finish_sorted<1>(out, lane);
     } else if (top_k <= 2 * kWave) {
       if constexpr (SE_CAP >= 2) finish_sorted<2>(out, lane);
@@ -312,6 +320,55 @@ struct WaveSelect {
     }
     wave_sort_desc<SE>(v, lane);
     write_out<SE>(v, out, lane);
+  }
+
+  // 2048 < top_k <= 4096: the held keys (cut to exactly top_k) are split into
+  // two runs of up to 2048 keys, each bitonic-sorted in registers and written
+  // back in rank order; then each lane merges 64 consecutive output ranks,
+  // its start in both runs found by a merge-path binary search.
+  __device__ __forceinline__ void sort_run(int base, int lane) {
+    uint64_t v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int pos = base + j * kWave + lane;
+      v[j] = pos < n ? buf[pos] : 0ull;
+    }
+    wave_sort_desc<32>(v, lane);
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < 32; ++j) buf[base + lane * 32 + j] = v[j];
+    wave_lds_sync();
+  }
+
+  __device__ __forceinline__ void finish_merged(const TopkRowOut& out, int lane) {
+    constexpr int L = 32 * kWave;  // run length
+    if (n > top_k) compact_to(lane, top_k, top_k);
+    wave_lds_sync();
+    sort_run(0, lane);
+    sort_run(L, lane);
+    const uint64_t* A = buf;
+    const uint64_t* Bv = buf + L;
+    // Output ranks [d, d + 64) of this lane: i of them come from run A.
+    const int d = lane * kWave;
+    int lo = d > L ? d - L : 0, hi = d < L ? d : L;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (A[mid] >= Bv[d - 1 - mid]) lo = mid + 1; else hi = mid;
+    }
+    int i = lo, j = d - lo;
+    for (int e = 0; e < kWave; ++e) {
+      const int o = d + e;
+      if (o >= top_k) break;
+      const uint64_t x = i < L ? A[i] : 0ull;
+      const uint64_t y = j < L ? Bv[j] : 0ull;
+      const bool ta = x >= y;
+      const uint64_t k = ta ? x : y;
+      i += ta ? 1 : 0;
+      j += ta ? 0 : 1;
+      if (out.idx64) out.idx64[o] = k ? static_cast<int64_t>(key_idx(k)) : int64_t(-1);
+      if (out.score) out.score[o] = k ? ord_to_f32(key_hi(k)) : -__builtin_inff();
+      if (out.idx32) out.idx32[o] = k ? static_cast<int32_t>(key_idx(k)) + out.off32 : int32_t(-1);
+    }
   }
 
   // Keys of rank lane*EE+j are staged through LDS in rank order so that the

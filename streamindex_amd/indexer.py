@@ -24,11 +24,10 @@ import torch
 from . import _lib
 
 SUPPORTED_D = (32, 64, 128, 256)
-MAX_HEADS = 128          # D_I <= 128
-MAX_HEADS_D256 = 64      # D_I = 256: the row's Q fragments take twice the registers
-MAX_TOPK = 2048
-MAX_TOPK_D256 = 1536     # D_I = 256: 32 KiB key tiles leave LDS for 2048-key selection buffers
+MAX_HEADS = 256          # any H_I up to 256 (rows past 128 heads, 64 at D_I = 256, split over waves)
+MAX_TOPK = 4096          # top_k above 2048 (1536 at D_I = 256) runs the head-split kernel
 MAX_HEADS_Q = 64         # fp4 q / fp8 k indexer
+MAX_TOPK_Q = 2048
 
 
 def _check_common(q: torch.Tensor, k_idx: torch.Tensor, weights: torch.Tensor):
@@ -45,9 +44,8 @@ def _check_common(q: torch.Tensor, k_idx: torch.Tensor, weights: torch.Tensor):
         raise ValueError(f"weights must be float32 or bfloat16, got {weights.dtype}")
     if D_I not in SUPPORTED_D:
         raise ValueError(f"D_I ({D_I}) must be one of {SUPPORTED_D}")
-    max_h = MAX_HEADS_D256 if D_I == 256 else MAX_HEADS
-    if H_I > max_h:
-        raise ValueError(f"H_I ({H_I}) must be <= {max_h} for D_I = {D_I}")
+    if H_I > MAX_HEADS:
+        raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS}")
     return B, S, H_I, D_I, T
 
 
@@ -90,9 +88,8 @@ def _topk_launch(q, k_idx, weights, top_k, causal_mask, causal_ratio):
     B, S, H_I, D_I, T = _check_common(q, k_idx, weights)
     if top_k <= 0:
         raise ValueError(f"top_k must be positive, got {top_k}")
-    max_k = MAX_TOPK_D256 if D_I == 256 else MAX_TOPK
-    if top_k > max_k:
-        raise ValueError(f"top_k ({top_k}) must be <= {max_k} for D_I = {D_I}")
+    if top_k > MAX_TOPK:
+        raise ValueError(f"top_k ({top_k}) must be <= {MAX_TOPK}")
     q, k_idx, weights = _prep(q, k_idx, weights)
     out_idx = torch.empty((B, S, top_k), dtype=torch.int64, device=q.device)
     out_scores = torch.empty((B, S, top_k), dtype=torch.float32, device=q.device)
@@ -240,8 +237,8 @@ def indexer_topk_q(
         raise ValueError(f"D_I ({D_I}) must be 128 for quantised inputs")
     if H_I > MAX_HEADS_Q:
         raise ValueError(f"H_I ({H_I}) must be <= {MAX_HEADS_Q} for quantised inputs")
-    if top_k <= 0 or top_k > MAX_TOPK:
-        raise ValueError(f"top_k must be in [1, {MAX_TOPK}], got {top_k}")
+    if top_k <= 0 or top_k > MAX_TOPK_Q:
+        raise ValueError(f"top_k must be in [1, {MAX_TOPK_Q}], got {top_k}")
     if check_scales and q_scale.numel():
         m, _ = torch.frexp(q_scale)
         if not bool((m == 0.5).all()):

@@ -29,7 +29,6 @@ import torch
 from . import _lib
 
 SUPPORTED_D = (32, 64, 128, 256, 512, 576)
-MAX_HEADS = 128
 
 
 def _check_device(dev: torch.device, **tensors) -> None:
@@ -82,8 +81,6 @@ def sparse_attn_fwd(
     assert topk_idxs.dim() == 3
     if D not in SUPPORTED_D:
         raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
-    if H > MAX_HEADS:
-        raise ValueError(f"H ({H}) must be <= {MAX_HEADS}")
     if topk_idxs.dtype not in (torch.int32, torch.int64):
         topk_idxs = topk_idxs.to(torch.int64)
     if softmax_scale is None:
@@ -167,8 +164,6 @@ def sparse_attn_bwd(
     assert q.dtype in (torch.bfloat16, torch.float16), f"Q must be bf16 or fp16, got {q.dtype}"
     if D not in SUPPORTED_D:
         raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
-    if H > MAX_HEADS:
-        raise ValueError(f"H ({H}) must be <= {MAX_HEADS}")
     if topk_idxs.dtype not in (torch.int32, torch.int64):
         topk_idxs = topk_idxs.to(torch.int64)
     if softmax_scale is None:

@@ -56,7 +56,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_version_and_workspace(lib):
-    assert lib.si_abi_version() == 7
+    assert lib.si_abi_version() == 8
     # the top-k kernel knob: previous mode returned, out-of-range rejected
     assert lib.si_indexer_set_topk_kernel(2) == 0
     assert lib.si_indexer_set_topk_kernel(1) == 2
@@ -91,9 +91,14 @@ def test_c_validation_codes_without_gpu(lib):
                              None, None, 1, 8, 4, 64, 48, 4, 4, fake, fake, None)
     assert rc == _lib.SI_ERR_UNSUPPORTED and b"D_I=48" in lib.si_last_error()
     # top_k beyond the kernel limit
-    rc = lib.si_indexer_topk(fake, qs, fake, ks, fake, 0, ws, None, None, 1, 8, 4, 64, 128, 4096, 4, fake, fake,
+    rc = lib.si_indexer_topk(fake, qs, fake, ks, fake, 0, ws, None, None, 1, 8, 4, 64, 128, 4097, 4, fake, fake,
                              None)
-    assert rc == _lib.SI_ERR_UNSUPPORTED
+    assert rc == _lib.SI_ERR_UNSUPPORTED and b"4096" in lib.si_last_error()
+    # H_I beyond the kernel limit
+    qs257 = _i64(8 * 257 * 128, 257 * 128, 128, 1)
+    rc = lib.si_indexer_topk(fake, qs257, fake, ks, fake, 0, _i64(8 * 257, 257, 1), None, None, 1, 8, 4, 257, 128,
+                             4, 4, fake, fake, None)
+    assert rc == _lib.SI_ERR_UNSUPPORTED and b"256" in lib.si_last_error()
     # sparse attention: unsupported head dim
     o4 = _i64(64 * 100, 64 * 100, 100, 1)
     rc = lib.si_sparse_attn_fwd(fake, o4, fake, _i64(100 * 16, 100, 1), fake, fake, 1, _i64(32, 8, 1),
@@ -110,6 +115,51 @@ def test_c_validation_codes_without_gpu(lib):
     # ... but a non-empty key set still needs its pointer
     rc = lib.si_indexer_topk(None, qs, None, ks, None, 0, ws, None, None, 1, 0, 4, 64, 128, 4, 4, None, None, None)
     assert rc == _lib.SI_ERR_INVALID
+
+
+def _plan(lib, S, T, H, D, top_k, ratio=0):
+    kern, cap = ctypes.c_int32(-1), ctypes.c_int32(-1)
+    rc = lib.si_indexer_topk_plan(S, T, H, D, top_k, ratio, ctypes.byref(kern), ctypes.byref(cap))
+    return rc, kern.value, cap.value
+
+
+NARROW_K, WIDE_K, SPLIT_K = 1, 2, 3
+
+
+def test_topk_dispatch_plan_without_gpu(lib):
+    """The dispatch of si_indexer_topk, read through si_indexer_topk_plan (no launch)."""
+    S = 1 << 16
+    # config[1]: two-workgroup kernel with the 1536-key buffer; S = 1M rows reach 64K legal keys: four-M-block
+    assert _plan(lib, S, S // 4, 64, 128, 512, 4) == (0, NARROW_K, 1536)
+    assert _plan(lib, 1 << 20, 1 << 18, 64, 128, 512, 4) == (0, WIDE_K, 1536)
+    # 128 heads at D = 128: four-M-block kernel, but never with fewer than 64 keys (its tile copies
+    # would re-read rows past T), whatever the forced mode
+    assert _plan(lib, 96, 300, 128, 128, 40)[:2] == (0, WIDE_K)
+    for T in (1, 37, 63):
+        assert _plan(lib, 96, T, 128, 128, 40)[:2] == (0, NARROW_K)
+    prev = lib.si_indexer_set_topk_kernel(2)
+    try:
+        assert _plan(lib, 96, 63, 64, 128, 40)[:2] == (0, NARROW_K)
+        assert _plan(lib, 96, 64, 64, 128, 40)[:2] == (0, WIDE_K)
+    finally:
+        lib.si_indexer_set_topk_kernel(prev)
+    # capacities of the two-workgroup kernel per top_k
+    for k, cap in ((32, 256), (33, 512), (192, 512), (193, 1536), (1152, 1536), (1153, 2048), (1536, 2048),
+                   (1537, 4096), (2048, 4096)):
+        assert _plan(lib, 96, 3000, 64, 128, k) == (0, NARROW_K, cap), k
+    # past what one wave holds: the head-split kernel
+    assert _plan(lib, 96, 3000, 192, 128, 512) == (0, SPLIT_K, 1536)
+    assert _plan(lib, 96, 3000, 256, 64, 2000) == (0, SPLIT_K, 4608)
+    assert _plan(lib, 96, 3000, 64, 128, 2049) == (0, SPLIT_K, 4608)
+    assert _plan(lib, 96, 3000, 64, 128, 4096) == (0, SPLIT_K, 4608)
+    assert _plan(lib, 96, 3000, 96, 256, 512) == (0, SPLIT_K, 1536)
+    assert _plan(lib, 96, 3000, 64, 256, 1537) == (0, SPLIT_K, 4608)
+    assert _plan(lib, 96, 3000, 256, 256, 4096) == (0, SPLIT_K, 4608)
+    # limits
+    assert _plan(lib, 96, 3000, 257, 128, 8)[0] == _lib.SI_ERR_UNSUPPORTED
+    assert _plan(lib, 96, 3000, 64, 128, 4097)[0] == _lib.SI_ERR_UNSUPPORTED
+    assert _plan(lib, 96, 3000, 64, 48, 8)[0] == _lib.SI_ERR_UNSUPPORTED
+    assert _plan(lib, 96, 3000, 64, 128, 0)[0] == _lib.SI_ERR_INVALID
 
 
 def test_csa_hca_validation_codes_without_gpu(lib):
@@ -130,7 +180,7 @@ def test_csa_hca_validation_codes_without_gpu(lib):
     ss = _i64(8 * 4, 4, 1)
     rc = lib.si_csa_scores_topk(fake, ss, 1, 8, 4, 0, 4, 8, 8, fake, os_, None)
     assert rc == _lib.SI_ERR_INVALID and b"top_k" in lib.si_last_error()
-    rc = lib.si_csa_scores_topk(fake, ss, 1, 8, 4, 4096, 4, 8, 8, fake, os_, None)
+    rc = lib.si_csa_scores_topk(fake, ss, 1, 8, 4, 4097, 4, 8, 8, fake, os_, None)
     assert rc == _lib.SI_ERR_UNSUPPORTED
     rc = lib.si_csa_scores_topk(fake, ss, 1, 0, 4, 16, 4, 8, 8, None, os_, None)  # empty: no launch
     assert rc == _lib.SI_OK

@@ -243,14 +243,14 @@ def test_invalid_arguments_raise(cuda_device):
         chunked_indexer_topk(q, k, w, 4, causal_mask=torch.ones(1, 16, 16, dtype=torch.bool, device="cuda"),
                              causal_ratio=4)
     with pytest.raises(ValueError):
-        chunked_indexer_topk(q, k, w, 4096)
+        chunked_indexer_topk(q, k, w, 4097)
     with pytest.raises(ValueError):
         chunked_indexer_topk(q.float(), k, w, 4)
     with pytest.raises(ValueError):
         q5, k5, w5 = _inputs(1, 16, 16, 48, 16, 3)
         chunked_indexer_topk(q5, k5, w5, 4)
-    # the limits of the wide shapes: H_I > 128, H_I > 64 at D_I = 256, top_k > 1536 at D_I = 256
-    for (H, D, kk) in ((160, 64, 4), (96, 256, 4), (32, 256, 2048)):
+    # the head limit: H_I > 256
+    for (H, D, kk) in ((257, 64, 4), (300, 256, 4)):
         qq, kk_, ww = _inputs(1, 8, H, D, 16, 4)
         with pytest.raises(ValueError):
             chunked_indexer_topk(qq, kk_, ww, kk)

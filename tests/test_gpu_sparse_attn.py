@@ -237,8 +237,10 @@ def test_tile_pipeline_depths(cuda_device, D, K, i64):
     _check(q, kv, sink, idx, D ** -0.5, o, lse, f"D={D} K={K}")
 
 
-@pytest.mark.parametrize("H", [16, 24, 64, 128])
+@pytest.mark.parametrize("H", [16, 24, 64, 128, 192, 256, 300])
 def test_head_counts(cuda_device, H):
+    # any H: one workgroup per 64-head group (the reference's cdiv(H, block_h)
+    # grid, sparse_attn_fwd.py:258); 300 leaves a partial fifth group
     B, S, D, N, K = 2, 10, 128, 64, 50
     q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=300 + H)
     g = torch.Generator().manual_seed(H)
@@ -246,6 +248,18 @@ def test_head_counts(cuda_device, H):
     o, lse = sparse_attn_fwd(q, kv, sink, idx, 0.1)
     torch.cuda.synchronize()
     _check(q, kv, sink, idx, 0.1, o, lse, f"H={H}")
+
+
+@pytest.mark.parametrize("H", [192, 136])
+def test_head_groups_v4_dim(cuda_device, H):
+    # D = 576 with three head groups (eight rows per workgroup) and int64 indices
+    B, S, D, N, K = 1, 40, 576, 300, 96
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N, seed=320 + H)
+    g = torch.Generator().manual_seed(320 + H)
+    idx = torch.randint(-1, N, (B, S, K), generator=g).cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx)
+    torch.cuda.synchronize()
+    _check(q, kv, sink, idx, D ** -0.5, o, lse, f"D=576 H={H}")
 
 
 def test_v4_shape_with_indexer_indices(cuda_device):

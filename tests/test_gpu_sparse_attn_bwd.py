@@ -108,7 +108,8 @@ def _run_and_check(B, S, H, D, N, K, seed, *, i64=False, mask_every=5, workspace
 
 
 @pytest.mark.parametrize("D,H,K,i64", [(64, 16, 64, False), (128, 64, 96, True), (576, 64, 64, False),
-                                       (32, 16, 40, True), (256, 80, 70, False), (512, 16, 33, True)])
+                                       (32, 16, 40, True), (256, 80, 70, False), (512, 16, 33, True),
+                                       (128, 192, 64, False), (576, 192, 40, True), (64, 260, 50, False)])
 def test_bwd_matches_oracle(cuda_device, D, H, K, i64):
     _run_and_check(2, 40, H, D, 200, K, seed=300 + D + H, i64=i64, label=f"D{D}H{H}K{K}")
 
