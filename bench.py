@@ -47,10 +47,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from streamindex_amd import (build_hca_topk_idxs, chunked_indexer_topk, csa_topk_idxs,  # noqa: E402
-                             flash_csa_forward, flash_hca_forward, sparse_attn, sparse_attn_bwd, sparse_attn_fwd)
+                             flash_csa_forward, flash_hca_forward, sparse_attn_bwd, sparse_attn_fwd,
+                             sparse_attn_kv2)
 from streamindex_amd import synth  # noqa: E402
 from streamindex_amd import _lib  # noqa: E402
-from streamindex_amd import sparse_attn as sparse_attn_mod  # noqa: E402
+import importlib  # noqa: E402
+
+# (the package re-exports the function sparse_attn under the module's name)
+sparse_attn_mod = importlib.import_module("streamindex_amd.sparse_attn")
 from streamindex_amd.csa import csa_row_len  # noqa: E402
 from streamindex_amd.hca import hca_row_len  # noqa: E402
 
@@ -575,7 +579,7 @@ def csa_attn_check(q, kv, kvc, sink, rows_gpu, nrows=8, seed=4):
     kv_full = torch.cat([kv[0], kvc[0]], dim=0)
     uniq = torch.unique(idx[idx >= 0])
     remap = torch.where(idx >= 0, torch.searchsorted(uniq, idx.clamp(min=0)), torch.full_like(idx, -1))
-    o = sparse_attn(q[:, sel], torch.cat([kv, kvc], dim=1), sink, rows_gpu[:, sel], None)
+    o = sparse_attn_kv2(q[:, sel], kv, kvc, sink, rows_gpu[:, sel], None)
     ro, _ = O.sparse_attn_rows(_bits(q[0, sel]), _bits(kv_full[uniq]), sink.cpu().numpy(), remap.cpu().numpy(),
                                D ** -0.5)
     return float(np.abs(o[0].float().cpu().numpy() - ro).max())
@@ -597,24 +601,22 @@ def run_csa_e2e(S, steps, warmup, parity_rows, n_h=64, d=576, H_I=64, D_I=128, m
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ms = _events_time(fn, steps, stream)
-    # stage split of one call (same three steps flash_csa_forward runs)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    # stage split of one call (the two steps flash_csa_forward runs; the
+    # attention reads kv and kv_compressed in place)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     ev[0].record(stream)
     rows_gpu = csa_topk_idxs(qi, ki, w, n_win=n_win, top_k=top_k, m=m, seq_len=S, quantized=quantized)
     row_len = csa_row_len(1, S, n_win, top_k, S // m, m, dev)
     ev[1].record(stream)
-    kv_full = torch.cat([kv, kvc], dim=1)
+    o = sparse_attn_kv2(q, kv, kvc, sink, rows_gpu, None, row_len=row_len)
     ev[2].record(stream)
-    o = sparse_attn(q, kv_full, sink, rows_gpu, None, row_len=row_len)
-    ev[3].record(stream)
     torch.cuda.synchronize()
-    del o, kv_full
+    del o
     nvalid = float((rows_gpu >= 0).sum().item())
     res = {
         "S": S, "T": S // m, "n_h": n_h, "d": d, "n_win": n_win, "top_k": top_k,
         "ms": ms, "peak_hbm_gib": peak,
-        "indexer_ms": ev[0].elapsed_time(ev[1]), "concat_ms": ev[1].elapsed_time(ev[2]),
-        "attn_ms": ev[2].elapsed_time(ev[3]),
+        "indexer_ms": ev[0].elapsed_time(ev[1]), "attn_ms": ev[1].elapsed_time(ev[2]),
         "indexer_flops": synth.indexer_flops(S, S // m, H_I, D_I, m),
         "attn_flops": 4.0 * n_h * d * nvalid,
     }
@@ -664,23 +666,20 @@ def run_hca_e2e(S, steps, warmup, check_rows, n_h=64, d=576, n_win=128, m_prime=
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ms = _events_time(fn, steps, stream)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     ev[0].record(stream)
     rows_gpu = build_hca_topk_idxs(B=1, seq_len=S, n_win=n_win, n_compressed=T, m_prime=m_prime, device=dev)
     row_len = hca_row_len(1, S, n_win, T, m_prime, dev)
     ev[1].record(stream)
-    kv_full = torch.cat([kv, kvc], dim=1)
+    o = sparse_attn_kv2(q, kv, kvc, sink, rows_gpu, None, row_len=row_len)
     ev[2].record(stream)
-    o = sparse_attn(q, kv_full, sink, rows_gpu, None, row_len=row_len)
-    ev[3].record(stream)
     torch.cuda.synchronize()
-    del o, kv_full
+    del o
     nvalid = float((rows_gpu >= 0).sum().item())
     K = n_win + T
     res = {
         "S": S, "T": T, "n_h": n_h, "d": d, "n_win": n_win, "m_prime": m_prime, "K": K, "ms": ms,
-        "rows_ms": ev[0].elapsed_time(ev[1]), "concat_ms": ev[1].elapsed_time(ev[2]),
-        "attn_ms": ev[2].elapsed_time(ev[3]),
+        "rows_ms": ev[0].elapsed_time(ev[1]), "attn_ms": ev[1].elapsed_time(ev[2]),
         "valid_frac": nvalid / (S * K),
         "attn_flops": 4.0 * n_h * d * nvalid,
     }

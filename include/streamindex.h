@@ -148,6 +148,22 @@ int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const voi
                               void* stream);
 
 /*
+ * si_sparse_attn_fwd_ragged over two KV tensors read in place: indices in
+ * [0, N_kv) select rows of kv [B,N_kv,D], indices in [N_kv, N_kv + N_kv2)
+ * rows of kv2 [B,N_kv2,D] (same element type, strides kv2_strides[3]).
+ * Equal to si_sparse_attn_fwd_ragged over their concatenation along N.
+ * topk_idxs is int32; each tensor's batch must be below 32 GiB.  Replaces
+ * the torch.cat([kv, kv_compressed]) that feeds sparse_attn_fwd in
+ * flash_sparse/csa.py:197-205 and flash_sparse/hca.py:85-95.
+ */
+int si_sparse_attn_fwd_kv2(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                           int64_t N_kv, const void* kv2, const int64_t* kv2_strides, int64_t N_kv2,
+                           const float* attn_sink, const int32_t* topk_idxs, const int64_t* idx_strides, int64_t B,
+                           int64_t S, int64_t H, int64_t D, int64_t K, float softmax_scale, int qkv_dtype, void* o,
+                           const int64_t* o_strides, float* lse, const int64_t* lse_strides, const int32_t* row_len,
+                           const int64_t* row_len_strides, void* stream);
+
+/*
  * Fused indexer top-k that writes CSA attention index rows directly.
  * Replaces flash_sparse/csa.py:149-179 (chunked indexer, window indices,
  * "+S" offset of the compressed picks, int32 concat) and, for the same

@@ -580,16 +580,3 @@ def set_overlap_recall(idx_a: np.ndarray, idx_b: np.ndarray) -> np.ndarray:
             out[r] = len(va & vb) / len(va)
     return out.reshape(lead)
 
-
-def boundary_gap(ref_scores_sorted: np.ndarray, all_scores: np.ndarray, lim: np.ndarray, top_k: int) -> np.ndarray:
-    """Gap between the k-th and (k+1)-th best legal score per row (inf when the
-    row has at most k legal keys)."""
-    n = all_scores.shape[0]
-    gap = np.full(n, np.inf)
-    for r in range(n):
-        L = int(lim[r])
-        if L <= top_k:
-            continue
-        row = np.sort(all_scores[r, :L])[::-1]
-        gap[r] = row[top_k - 1] - row[top_k]
-    return gap

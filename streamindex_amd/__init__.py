@@ -22,7 +22,8 @@ The same names are importable under the reference's module paths through the
 
 from .indexer import (chunked_indexer_topk, chunked_indexer_topk_quantized, indexer_score, indexer_score_topk,
                       indexer_topk_q)
-from .sparse_attn import build_inverted_topk, sparse_attn, sparse_attn_bwd, sparse_attn_bwd_v2, sparse_attn_fwd
+from .sparse_attn import (build_inverted_topk, sparse_attn, sparse_attn_bwd, sparse_attn_bwd_v2, sparse_attn_fwd,
+                          sparse_attn_fwd_kv2, sparse_attn_kv2)
 from .csa import build_csa_topk_idxs, csa_topk_idxs, flash_csa_forward
 from .hca import build_hca_topk_idxs, flash_hca_forward
 
@@ -39,6 +40,8 @@ __all__ = [
     "sparse_attn_bwd_v2",
     "build_inverted_topk",
     "sparse_attn_fwd",
+    "sparse_attn_fwd_kv2",
+    "sparse_attn_kv2",
     "flash_csa_forward",
     "build_csa_topk_idxs",
     "csa_topk_idxs",

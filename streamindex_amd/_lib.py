@@ -50,6 +50,9 @@ SIGNATURES = {
     "si_sparse_attn_fwd_ragged": (_I32, [_P, _I64P, _P, _I64P, _P, _P, _I32, _I64P,
                                          _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
                                          _P, _I64P, _P, _I64P, _P, _I64P, _P]),
+    "si_sparse_attn_fwd_kv2": (_I32, [_P, _I64P, _P, _I64P, _I64, _P, _I64P, _I64, _P, _P, _I64P,
+                                      _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I32,
+                                      _P, _I64P, _P, _I64P, _P, _I64P, _P]),
     "si_indexer_topk_q": (_I32, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I32, _I64P, _P, _I64P,
                                  _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "si_csa_indexer_topk_q": (_I32, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I32, _I64P,

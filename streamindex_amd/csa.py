@@ -28,7 +28,10 @@ Deliberate differences (documented for drop-in users):
   every setting yields the same indices.
 * Ties among equal scores rank the smaller compressed index first
   (``torch.topk`` leaves tie order unspecified).
-* Gradients flow through ``sparse_attn``'s autograd (the HIP backward) into
+* The attention reads ``kv`` and ``kv_compressed`` in place (two base
+  pointers, :func:`streamindex_amd.sparse_attn.sparse_attn_fwd_kv2`) instead
+  of the reference's ``torch.cat`` of the two (``csa.py:197-205``).
+* Gradients flow through the sparse-attention autograd (the HIP backward) into
   ``q``, ``kv`` / ``kv_compressed`` and ``attn_sink``; the index rows carry none.
 """
 
@@ -40,7 +43,7 @@ import torch
 
 from . import _lib
 from .indexer import _check_common, _prep, MAX_HEADS_Q, MAX_TOPK, MAX_TOPK_Q
-from .sparse_attn import sparse_attn
+from .sparse_attn import sparse_attn_kv2
 
 __all__ = ["flash_csa_forward", "build_csa_topk_idxs", "csa_topk_idxs", "build_sliding_window_idxs", "csa_row_len"]
 
@@ -204,9 +207,9 @@ def flash_csa_forward(
         raise ValueError(f"chunk_s and chunk_t must be positive, got {chunk_s}, {chunk_t}")
     topk_idxs = csa_topk_idxs(q_idx, k_idx_compressed, indexer_weights, n_win=n_win, top_k=top_k, m=m,
                               seq_len=S, quantized=quantized_indexer)
-    kv_full = torch.cat([kv, kv_compressed], dim=1)
     row_len = csa_row_len(B, S, n_win, top_k, n_compressed, m, q.device)
-    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+    # the rows index [kv ; kv_compressed]; the kernel reads both in place
+    return sparse_attn_kv2(q, kv, kv_compressed, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
 
 
 def csa_row_len(B: int, S: int, n_win: int, top_k: int, n_compressed: int, m: int, device) -> torch.Tensor:

@@ -69,6 +69,12 @@ struct SparseAttnArgs {
   int HG;              // head groups of 64
   float scale_log2;    // softmax_scale * log2(e)
   int f16;             // element type: 0 bf16, 1 fp16
+  // Optional second KV tensor [B,N-N1,D] (kernel instantiation KV2): indices
+  // in [N1, N) select its row index - N1, so a [kv ; kv_compressed] layout
+  // needs no concatenated copy.
+  const uint16_t* kv2;
+  int64_t kv2sb, kv2sn;
+  int N1;
 };
 
 // The reference maximum of a head moves only when a tile's maximum exceeds it
@@ -97,7 +103,11 @@ constexpr int attn_rows_per_workgroup() {
   return D >= 512 ? 8 : 1;
 }
 
-template <int D, bool IDX64, bool F16>
+// With KV2 a published row offset carries the tensor in bit 31 (set: the
+// second KV tensor); each tensor's batch holds at most 2^31 16-byte units.
+constexpr uint32_t kKv2Bit = 0x80000000u;
+
+template <int D, bool IDX64, bool F16, bool KV2>
 __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
   constexpr int kAttnRows = attn_rows_per_workgroup<D>();
   using SH = AttnShape<D>;
@@ -183,6 +193,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       // ---- KV gather (issued by the producers, which wait at the tile barrier
       // for the P.V waves otherwise) -------------------------------------------
       const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
+      const char* kvb2 = KV2 ? reinterpret_cast<const char*>(a.kv2 + b * a.kv2sb) : kvb;
       // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
       // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
       // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
@@ -209,7 +220,13 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
         // (passed as uint16_t*: a char* argument to this builtin makes clang
         // drop the host launch stubs of later instantiations)
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+        const uint16_t* src;
+        if constexpr (KV2) {
+          const char* base = (roff[i] & kKv2Bit) ? kvb2 : kvb;
+          src = reinterpret_cast<const uint16_t*>(base + (static_cast<uint64_t>(roff[i] & ~kKv2Bit) << 4));
+        } else {
+          src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+        }
         if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
           __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
         } else if (e0 < SH::CH) {
@@ -444,7 +461,14 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
           const int j = t * kAttnTK + lane;
           const bool ok = j < klen && raw >= 0 && raw < a.N;
           bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
-          rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
+          if constexpr (KV2) {
+            const bool second = raw >= a.N1;
+            rowoff_lds[slot][lane] = !ok ? 0u
+                                     : second ? (kKv2Bit | static_cast<uint32_t>((raw - a.N1) * (a.kv2sn / 8)))
+                                              : static_cast<uint32_t>(raw * (a.kvsn / 8));
+          } else {
+            rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
+          }
         }
       };
       // V^T transposing-read address: source lane (g, i16) points at key
@@ -593,12 +617,15 @@ static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
   const int64_t nblk = static_cast<int64_t>(a.B) * ((a.S + R - 1) / R) * a.HG;
   if (nblk > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
   const dim3 grid(static_cast<unsigned>(nblk)), block(kAttnThreads);
-  if (a.f16) {
-    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, true>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, true>), grid, block, 0, st, a);
+  if (a.kv2) {  // (int32 indices: the CSA / HCA rows)
+    if (a.f16) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, true, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, false, true>), grid, block, 0, st, a);
+  } else if (a.f16) {
+    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, true, false>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, true, false>), grid, block, 0, st, a);
   } else {
-    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, false>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, false>), grid, block, 0, st, a);
+    if (a.idx64) hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, true, false, false>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sparse_attn_fwd_kernel<D, false, false, false>), grid, block, 0, st, a);
   }
   return check_launch("sparse_attn_fwd_kernel");
 }
@@ -607,12 +634,15 @@ static int launch_attn(const SparseAttnArgs& a, hipStream_t st) {
 
 using namespace si;
 
-extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv,
-                                         const int64_t* kv_strides, const float* attn_sink, const void* topk_idxs,
-                                         int idx_is_i64, const int64_t* idx_strides, int64_t B, int64_t S, int64_t H,
-                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype,
-                                         void* o, const int64_t* o_strides, float* lse, const int64_t* lse_strides,
-                                         const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
+// Shared body of the forward entries.  kv2 (with N_kv2 rows) is the optional
+// second KV tensor: indices in [N_kv, N_kv + N_kv2) select its rows.
+static int sparse_attn_fwd_entry(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,
+                                 int64_t N_kv, const void* kv2, const int64_t* kv2_strides, int64_t N_kv2,
+                                 const float* attn_sink, const void* topk_idxs, int idx_is_i64,
+                                 const int64_t* idx_strides, int64_t B, int64_t S, int64_t H, int64_t D, int64_t K,
+                                 float softmax_scale, int qkv_dtype, void* o, const int64_t* o_strides, float* lse,
+                                 const int64_t* lse_strides, const int32_t* row_len, const int64_t* row_len_strides,
+                                 void* stream) {
   if (row_len && !row_len_strides) return set_error(SI_ERR_INVALID, "null row_len strides");
   if (qkv_dtype != SI_DTYPE_BF16 && qkv_dtype != SI_DTYPE_F16)
     return set_error(SI_ERR_INVALID, "qkv_dtype must be SI_DTYPE_BF16 (0) or SI_DTYPE_F16 (1)");
@@ -634,10 +664,29 @@ extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kv)) & 15)
     return set_error(SI_ERR_INVALID, "q/kv must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(o) & 15) return set_error(SI_ERR_INVALID, "o must be 16-byte aligned");
-  // KV row offsets are kept in 32 bits, in 16-byte units, inside one batch.
-  if (N_kv > 0 && ((N_kv - 1) * kv_strides[1] + D) / 8 >= (int64_t{1} << 32))
-    return set_error(SI_ERR_UNSUPPORTED, "kv batch larger than 64 GiB");
+  // KV row offsets are kept in 32 bits, in 16-byte units, inside one batch
+  // (31 bits per tensor with a second KV tensor).
+  const int off_bits = kv2 ? 31 : 32;
+  if (N_kv > 0 && ((N_kv - 1) * kv_strides[1] + D) / 8 >= (int64_t{1} << off_bits))
+    return set_error(SI_ERR_UNSUPPORTED, kv2 ? "kv batch larger than 32 GiB" : "kv batch larger than 64 GiB");
+  if (kv2) {
+    if (!kv2_strides) return set_error(SI_ERR_INVALID, "null stride argument");
+    if (N_kv2 < 0) return set_error(SI_ERR_INVALID, "bad dimension");
+    if (N_kv + N_kv2 > 0x7fffffff) return set_error(SI_ERR_UNSUPPORTED, "dimension exceeds int32");
+    if (idx_is_i64) return set_error(SI_ERR_UNSUPPORTED, "two KV tensors take int32 indices");
+    if (kv2_strides[2] != 1 || (kv2_strides[0] | kv2_strides[1]) % 8 || (reinterpret_cast<uintptr_t>(kv2) & 15))
+      return set_error(SI_ERR_INVALID, "kv2 needs a contiguous last dimension, 16-byte rows and alignment");
+    if (N_kv2 > 0 && ((N_kv2 - 1) * kv2_strides[1] + D) / 8 >= (int64_t{1} << 31))
+      return set_error(SI_ERR_UNSUPPORTED, "kv2 batch larger than 32 GiB");
+  }
   SparseAttnArgs a{};
+  if (kv2 && N_kv2 > 0) {
+    a.kv2 = static_cast<const uint16_t*>(kv2);
+    a.kv2sb = kv2_strides[0];
+    a.kv2sn = kv2_strides[1];
+    a.N1 = static_cast<int>(N_kv);
+    N_kv += N_kv2;
+  }
   a.q = static_cast<const uint16_t*>(q);
   a.qsb = q_strides[0]; a.qss = q_strides[1]; a.qsh = q_strides[2];
   a.kv = static_cast<const uint16_t*>(kv);
@@ -673,6 +722,31 @@ extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides
       return set_error(SI_ERR_UNSUPPORTED,
                        "unsupported head dim D=" + std::to_string(D) + " (supported: 32, 64, 128, 256, 512, 576)");
   }
+}
+
+extern "C" int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const void* kv,
+                                         const int64_t* kv_strides, const float* attn_sink, const void* topk_idxs,
+                                         int idx_is_i64, const int64_t* idx_strides, int64_t B, int64_t S, int64_t H,
+                                         int64_t D, int64_t N_kv, int64_t K, float softmax_scale, int qkv_dtype,
+                                         void* o, const int64_t* o_strides, float* lse, const int64_t* lse_strides,
+                                         const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
+  return sparse_attn_fwd_entry(q, q_strides, kv, kv_strides, N_kv, nullptr, nullptr, 0, attn_sink, topk_idxs,
+                               idx_is_i64, idx_strides, B, S, H, D, K, softmax_scale, qkv_dtype, o, o_strides, lse,
+                               lse_strides, row_len, row_len_strides, stream);
+}
+
+extern "C" int si_sparse_attn_fwd_kv2(const void* q, const int64_t* q_strides, const void* kv,
+                                      const int64_t* kv_strides, int64_t N_kv, const void* kv2,
+                                      const int64_t* kv2_strides, int64_t N_kv2, const float* attn_sink,
+                                      const int32_t* topk_idxs, const int64_t* idx_strides, int64_t B, int64_t S,
+                                      int64_t H, int64_t D, int64_t K, float softmax_scale, int qkv_dtype, void* o,
+                                      const int64_t* o_strides, float* lse, const int64_t* lse_strides,
+                                      const int32_t* row_len, const int64_t* row_len_strides, void* stream) {
+  if (B > 0 && S > 0 && N_kv2 > 0 && !kv2) return set_error(SI_ERR_INVALID, "null pointer argument");
+  // (a null kv2 with no rows is the one-tensor case)
+  return sparse_attn_fwd_entry(q, q_strides, kv, kv_strides, N_kv, N_kv2 > 0 ? kv2 : nullptr, kv2_strides, N_kv2,
+                               attn_sink, topk_idxs, 0, idx_strides, B, S, H, D, K, softmax_scale, qkv_dtype, o,
+                               o_strides, lse, lse_strides, row_len, row_len_strides, stream);
 }
 
 extern "C" int si_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* kv, const int64_t* kv_strides,

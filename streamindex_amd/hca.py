@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 from .csa import _launch_hca
-from .sparse_attn import sparse_attn
+from .sparse_attn import sparse_attn_kv2
 
 __all__ = ["flash_hca_forward", "build_hca_topk_idxs", "hca_row_len"]
 
@@ -67,9 +67,9 @@ def flash_hca_forward(
     assert q.is_cuda
     topk_idxs = build_hca_topk_idxs(B=B, seq_len=S, n_win=n_win, n_compressed=n_compressed, m_prime=m_prime,
                                     device=q.device)
-    kv_full = torch.cat([kv, kv_compressed], dim=1)
     row_len = hca_row_len(B, S, n_win, n_compressed, m_prime, q.device)
-    return sparse_attn(q, kv_full, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+    # the rows index [kv ; kv_compressed]; the kernel reads both in place
+    return sparse_attn_kv2(q, kv, kv_compressed, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
 
 
 def hca_row_len(B: int, S: int, n_win: int, n_compressed: int, m_prime: int, device) -> torch.Tensor:

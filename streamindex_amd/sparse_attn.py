@@ -113,6 +113,63 @@ def sparse_attn_fwd(
     return o, lse
 
 
+def sparse_attn_fwd_kv2(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    kv2: torch.Tensor,
+    attn_sink: torch.Tensor,
+    topk_idxs: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    *,
+    row_len: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """:func:`sparse_attn_fwd` over the rows of ``[kv ; kv2]`` (concatenated
+    along N) without building that tensor: index ``j < N1`` reads ``kv[:, j]``,
+    ``N1 <= j < N1 + N2`` reads ``kv2[:, j - N1]``.  The CSA / HCA layout
+    (``flash_sparse/csa.py:197-205``, ``hca.py:85-95``: window columns into
+    the uncompressed KV, picks ``+ S`` into the compressed KV).  An extension
+    with no reference counterpart; ``topk_idxs`` is int32 (the compositions'
+    rows), other integer types are converted.  Same outputs as
+    ``sparse_attn_fwd(q, torch.cat([kv, kv2], 1), ...)``.
+    """
+    assert q.is_cuda and kv.is_cuda and kv2.is_cuda
+    _check_device(q.device, kv=kv, kv2=kv2, attn_sink=attn_sink, topk_idxs=topk_idxs, row_len=row_len)
+    assert q.dim() == 4 and kv.dim() == 3 and kv2.dim() == 3
+    assert q.dtype in (torch.bfloat16, torch.float16), f"Q must be bf16 or fp16, got {q.dtype}"
+    assert kv.dtype == q.dtype and kv2.dtype == q.dtype
+    assert attn_sink.dtype == torch.float32
+    B, S, H, D = q.shape
+    N1, N2 = kv.shape[1], kv2.shape[1]
+    assert kv.shape == (B, N1, D) and kv2.shape == (B, N2, D), "q, kv and kv2 shape mismatch"
+    assert attn_sink.shape == (H,)
+    assert topk_idxs.dim() == 3 and topk_idxs.shape[:2] == (B, S)
+    if D not in SUPPORTED_D:
+        raise ValueError(f"D ({D}) must be one of {SUPPORTED_D}")
+    if topk_idxs.dtype != torch.int32:
+        topk_idxs = topk_idxs.to(torch.int32)
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    K = topk_idxs.shape[-1]
+    q, kv, kv2 = (t if _aligned(t) else t.contiguous() for t in (q, kv, kv2))
+    attn_sink = attn_sink.contiguous()
+    if row_len is not None:
+        assert row_len.is_cuda and row_len.shape == (B, S), "row_len must be [B, S] on the GPU"
+        if row_len.dtype != torch.int32:
+            row_len = row_len.to(torch.int32)
+    o = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=q.device)
+    L = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = L.si_sparse_attn_fwd_kv2(
+            q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), N1, kv2.data_ptr(), _lib.strides(kv2),
+            N2, attn_sink.data_ptr(), topk_idxs.data_ptr(), _lib.strides(topk_idxs), B, S, H, D, K,
+            float(softmax_scale), _lib.qkv_dtype(q), o.data_ptr(), _lib.strides(o), lse.data_ptr(),
+            _lib.strides(lse), None if row_len is None else row_len.data_ptr(),
+            None if row_len is None else _lib.strides(row_len), _lib.stream_ptr(q.device))
+    _lib.check(rc)
+    return o, lse
+
+
 # Default cap on the backward's workspace: at most this, and at most a quarter
 # of the device memory free at the call (the driver's free memory plus what
 # the caching allocator holds unused).
@@ -180,6 +237,7 @@ def sparse_attn_bwd(
     dsink = torch.empty((H,), dtype=torch.float32, device=q.device)
     L = _lib.load()
     with torch.cuda.device(q.device):
+        default_cap = workspace_bytes is None
         if workspace_bytes is None:
             # Memory the caching allocator holds but has not handed out counts
             # as free too: the driver's free figure alone moves with every
@@ -191,7 +249,18 @@ def sparse_attn_bwd(
         need = L.si_sparse_attn_bwd_workspace_bytes(B, S, H, D, N_kv, K, int(workspace_bytes))
         if need < 0:
             raise ValueError(L.si_last_error().decode("utf-8", "replace"))
-        ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=q.device)
+        try:
+            ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=q.device)
+        except torch.OutOfMemoryError:
+            if not default_cap:
+                raise
+            # The allocator's unused blocks may be split too finely to hold the
+            # workspace: size it from the driver's free memory alone.
+            free, _ = torch.cuda.mem_get_info(q.device)
+            need = L.si_sparse_attn_bwd_workspace_bytes(B, S, H, D, N_kv, K, int(min(BWD_WORKSPACE_CAP, free // 4)))
+            if need < 0:
+                raise ValueError(L.si_last_error().decode("utf-8", "replace"))
+            ws = torch.empty((max(int(need), 16),), dtype=torch.uint8, device=q.device)
         rc = L.si_sparse_attn_bwd_ragged(
             q.data_ptr(), _lib.strides(q), kv.data_ptr(), _lib.strides(kv), attn_sink.data_ptr(),
             topk_idxs.data_ptr(), 1 if topk_idxs.dtype == torch.int64 else 0, _lib.strides(topk_idxs),
@@ -269,6 +338,34 @@ class _SparseAttnFunc(torch.autograd.Function):
         return dq, dkv, dsink, None, None, None
 
 
+class _SparseAttnKV2Func(torch.autograd.Function):
+    """Autograd over two KV tensors: the forward reads both in place; the
+    backward (which reads every selected row several times over anyway)
+    runs on their concatenation and splits dkv."""
+
+    @staticmethod
+    def forward(ctx, q, kv, kv2, attn_sink, topk_idxs, softmax_scale, row_len):
+        o, lse = sparse_attn_fwd_kv2(q, kv, kv2, attn_sink, topk_idxs, softmax_scale, row_len=row_len)
+        ctx.save_for_backward(q, kv, kv2, attn_sink, topk_idxs, o, lse, row_len)
+        ctx.softmax_scale = softmax_scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, kv, kv2, attn_sink, topk_idxs, o, lse, row_len = ctx.saved_tensors
+        n1 = kv.shape[1]
+        dq, dkv, dsink = sparse_attn_bwd(q, torch.cat([kv, kv2], dim=1), attn_sink, topk_idxs, o, lse,
+                                         do.contiguous(), ctx.softmax_scale, row_len=row_len)
+        return dq, dkv[:, :n1], dkv[:, n1:], dsink, None, None, None
+
+
+def sparse_attn_kv2(q, kv, kv2, attn_sink, topk_idxs, softmax_scale: Optional[float] = None, *,
+                    row_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Differentiable :func:`sparse_attn_fwd_kv2` returning ``o`` (an extension used by the
+    CSA / HCA compositions)."""
+    return _SparseAttnKV2Func.apply(q, kv, kv2, attn_sink, topk_idxs, softmax_scale, row_len)
+
+
 def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = None, *,
                 row_len: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Differentiable sparse attention returning ``o`` only (``flash_sparse/triton/__init__.py:48-60``).
@@ -276,4 +373,5 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: Optional[float] = No
     return _SparseAttnFunc.apply(q, kv, attn_sink, topk_idxs, softmax_scale, row_len)
 
 
-__all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn_bwd_v2", "sparse_attn", "build_inverted_topk"]
+__all__ = ["sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn_bwd_v2", "sparse_attn", "build_inverted_topk",
+           "sparse_attn_fwd_kv2", "sparse_attn_kv2"]

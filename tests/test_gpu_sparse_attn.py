@@ -282,3 +282,55 @@ def test_sparse_attn_matches_fwd(cuda_device):
     o = sparse_attn(q, kv, sink, idx)
     o2, _ = sparse_attn_fwd(q, kv, sink, idx)
     assert torch.equal(o, o2)
+
+
+@pytest.mark.parametrize("D,H,f16", [(576, 64, False), (128, 16, True), (64, 80, False), (512, 130, False)])
+def test_two_kv_tensors(cuda_device, D, H, f16):
+    # [kv ; kv2] read in place (the CSA / HCA layout): bit-identical to the
+    # forward over their concatenation, with per-row column counts, a strided
+    # second tensor and indices past N (masked); gradients through the
+    # two-tensor autograd equal those of the concatenated one.
+    from streamindex_amd import sparse_attn_fwd_kv2, sparse_attn_kv2
+
+    B, S, N1, N2, K = 2, 48, 100, 37, 96
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N1, seed=400 + D)
+    _, big, _ = synth.sparse_attn_inputs(B, 1, 1, D, 2 * N2, seed=401 + D)
+    kv2 = big[:, ::2]  # row stride 2 D
+    if f16:
+        q, kv, kv2 = q.half(), kv.half(), kv2.half()
+    g = torch.Generator().manual_seed(D + H)
+    idx = torch.randint(-1, N1 + N2 + 3, (B, S, K), generator=g, dtype=torch.int32).cuda()
+    rl = torch.randint(0, K + 5, (B, S), generator=g, dtype=torch.int32).cuda()
+    kv_cat = torch.cat([kv, kv2], dim=1)
+    for row_len in (None, rl):
+        o1, l1 = sparse_attn_fwd_kv2(q, kv, kv2, sink, idx, row_len=row_len)
+        o2, l2 = sparse_attn_fwd(q, kv_cat, sink, idx, row_len=row_len)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    if not f16:
+        o1, l1 = sparse_attn_fwd_kv2(q, kv, kv2, sink, idx)
+        _check(q, kv_cat, sink, idx, D ** -0.5, o1, l1, f"kv2 D={D}")
+    leaves = [t.detach().requires_grad_() for t in (q, kv, kv2, sink)]
+    o = sparse_attn_kv2(leaves[0], leaves[1], leaves[2], leaves[3], idx, row_len=rl)
+    do = torch.randn(o.shape, generator=g).to(o.dtype).cuda()
+    g1 = torch.autograd.grad(o, leaves, do)
+    leaves2 = [t.detach().requires_grad_() for t in (q, kv_cat, sink)]
+    o2 = sparse_attn(leaves2[0], leaves2[1], leaves2[2], idx, row_len=rl)
+    g2 = torch.autograd.grad(o2, leaves2, do)
+    assert torch.equal(o, o2)
+    assert torch.equal(g1[0], g2[0]) and torch.equal(g1[3], g2[2])
+    assert torch.equal(torch.cat([g1[1], g1[2]], dim=1), g2[1])
+
+
+def test_two_kv_empty_second(cuda_device):
+    # no rows in the second tensor: the one-tensor path; indices past N1 masked
+    from streamindex_amd import sparse_attn_fwd_kv2
+
+    B, S, H, D, N1, K = 1, 16, 16, 64, 40, 32
+    q, kv, sink = synth.sparse_attn_inputs(B, S, H, D, N1, seed=410)
+    kv2 = torch.empty(B, 0, D, dtype=kv.dtype, device=kv.device)
+    idx = torch.randint(-1, N1 + 4, (B, S, K), generator=torch.Generator().manual_seed(1), dtype=torch.int32).cuda()
+    o1, l1 = sparse_attn_fwd_kv2(q, kv, kv2, sink, idx)
+    o2, l2 = sparse_attn_fwd(q, kv, sink, idx)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
