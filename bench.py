@@ -466,7 +466,8 @@ def attn_parity(q, kv, sink, idx, o, lse, nrows=64, seed=33):
     return {"rows": int(len(rows)), "o_max_abs_err": oe, "lse_max_abs_err": le, "pass": bool(oe <= 2e-2 and le <= 2e-3)}
 
 
-def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True, parity_rows=0):
+def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=True, parity_rows=0, bwd_cap=None,
+                    sweep=True):
     """Forward (and optionally backward) sparse attention at one shape, on the
     given indices (config[3]: config[1]'s indexer output) or on random distinct
     causal ones.  The backward is timed from the forward's saved (o, lse) with
@@ -498,7 +499,7 @@ def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=T
         g = torch.Generator(device=dev)
         g.manual_seed(2028)
         do = torch.randn(q.shape, generator=g, device=dev, dtype=torch.bfloat16).mul_(0.5)
-        def bfn(cap=None):
+        def bfn(cap=bwd_cap):
             return sparse_attn_bwd(q, kv, sink, idx, o, lse, do, D ** -0.5, workspace_bytes=cap)
 
         for _ in range(max(1, warmup)):
@@ -509,14 +510,14 @@ def run_sparse_attn(S, T, H, D, top_k, steps, warmup, idx=None, bwd=False, fwd=T
         # memory one call adds beyond its inputs: dq, dkv, dsink and the workspace
         res["bwd_peak_extra_gib"] = _peak_gib(bfn)
         res["bwd_workspace_cap_gib"] = sparse_attn_mod.BWD_WORKSPACE_CAP / 2 ** 30
-        sweep = []
-        for cap_gib in BWD_SWEEP_GIB:
+        swept = []
+        for cap_gib in (BWD_SWEEP_GIB if sweep else ()):
             f = lambda: bfn(cap_gib << 30)  # noqa: E731
             f()
             torch.cuda.synchronize()
-            sweep.append({"workspace_cap_gib": cap_gib, "ms": _events_time(f, max(3, steps // 2), stream),
+            swept.append({"workspace_cap_gib": cap_gib, "ms": _events_time(f, max(3, steps // 2), stream),
                           "peak_extra_gib": _peak_gib(f)})
-        res["bwd_workspace_sweep"] = sweep
+        res["bwd_workspace_sweep"] = swept
         res["bwd_parity"] = attn_bwd_check(q, kv, sink, idx, o, lse, do, bfn())
     return res
 
@@ -734,6 +735,8 @@ def main():
     ap.add_argument("--only-attn-random", action="store_true",
                     help="sparse-attention timing on random causal indices only (for profilers)")
     ap.add_argument("--only-attn-bwd", action="store_true", help="sparse-attention backward timing only (for profilers)")
+    ap.add_argument("--bwd-workspace-gib", type=float, default=0.0, metavar="GIB",
+                    help="with --only-attn-bwd: cap the backward's workspace at GIB (default: the library's cap)")
     ap.add_argument("--only-indexer-q", type=int, default=0, metavar="S",
                     help="fp4/fp8 indexer timing only at sequence length S (for profilers)")
     ap.add_argument("--no-indexer-q", action="store_true", help="skip the fp4/fp8 indexer measurements")
@@ -776,9 +779,11 @@ def main():
         ri = run_indexer(65536, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
         idx = ri["idx"]
         del ri
-        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, idx=idx, bwd=True, fwd=False)
+        cap = int(args.bwd_workspace_gib * (1 << 30)) if args.bwd_workspace_gib > 0 else None
+        ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, idx=idx, bwd=True, fwd=False,
+                             bwd_cap=cap, sweep=False)
         print(json.dumps({"sparse_attn_bwd_ms": ra["bwd_ms"], "tflops": ra["bwd_flops"] / ra["bwd_ms"] / 1e9,
-                          "parity": ra["bwd_parity"]}), flush=True)
+                          "peak_extra_gib": ra["bwd_peak_extra_gib"], "parity": ra["bwd_parity"]}), flush=True)
         return
     if args.only_attn or args.only_attn_random:
         idx = None

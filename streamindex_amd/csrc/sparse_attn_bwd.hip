@@ -671,13 +671,14 @@ __global__ __launch_bounds__(kRowsThreads) void sparse_attn_bwd_dkv_rows_kernel(
 // 3. key-major reduction of the dkv rows
 // ---------------------------------------------------------------------------
 struct DkvReduceArgs {
-  const uint32_t* pair;   // local pair ids (lrow K + j) sorted by key
-  const int32_t* seg_lo;  // per key id b N + t: its pairs are pair[seg_lo, seg_hi)
+  const uint32_t* pair;   // pair ids of the sort group (lrow K + j, lrow counted from the group's first row)
+  const int32_t* seg_lo;  // per key id b N + t: its pairs in this chunk are pair[seg_lo, seg_hi)
   const int32_t* seg_hi;
   const uint16_t* prow;   // [nrows, HG, KP, D]
   float* acc;             // [B N, D] running fp32 sum across chunks
   uint16_t* dkv;          // [B, N, D] bf16
   int64_t dsb, dsn;
+  int64_t prow0;          // the chunk's first row, counted from the group's first row
   int K, KP, HG, N;      // KP: slots per (row, head group), K rounded up to whole tiles
   int first, last;        // first / last chunk of query rows
 };
@@ -705,12 +706,25 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
   const int kid = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
   const int grp = threadIdx.x / CPR;
   const int c = threadIdx.x % CPR;
+  float* accp = r.acc + static_cast<int64_t>(kid) * D + c * 8;
+  // The running sum of the earlier chunks is read first, so that its load
+  // overlaps the segment's row loads instead of following them.
+  float prev[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (!r.first && threadIdx.x < CPR) {
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(accp);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(accp + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      prev[e] = a0[e];
+      prev[4 + e] = a1[e];
+    }
+  }
   float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
     const int lo = r.seg_lo[kid], hi = r.seg_hi[kid];
     auto add_row = [&](int p) {
       const uint32_t pid = r.pair[p];
-      const int64_t lrow = pid / static_cast<uint32_t>(r.K);
+      const int64_t lrow = pid / static_cast<uint32_t>(r.K) - r.prow0;
       const int64_t j = pid % static_cast<uint32_t>(r.K);
       for (int h = 0; h < r.HG; ++h) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(r.prow + ((lrow * r.HG + h) * r.KP + j) * D + c * 8);
@@ -732,7 +746,7 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
           u32x4 v[8];
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            const int64_t lrow = pid[u] / static_cast<uint32_t>(r.K);
+            const int64_t lrow = pid[u] / static_cast<uint32_t>(r.K) - r.prow0;
             const int64_t j = pid[u] % static_cast<uint32_t>(r.K);
             v[u] = *reinterpret_cast<const u32x4*>(r.prow + (lrow * r.KP + j) * D + c * 8);
           }
@@ -766,10 +780,9 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
       for (int q = 0; q < G; ++q) v += red[q * D + c * 8 + e];
       tot[e] = v;
     }
-    float* accp = r.acc + static_cast<int64_t>(kid) * D + c * 8;
     if (!r.first) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tot[e] += accp[e];
+      for (int e = 0; e < 8; ++e) tot[e] += prev[e];
     }
     if (!r.last) {
 #pragma unroll
@@ -784,12 +797,15 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
   }
 }
 
-// Sort keys and payloads of the chunk's (query, slot) pairs: key b N + t for
-// a valid index t, the sentinel B N (sorted last, never reduced) otherwise.
+// Sort keys and payloads of a sort group's (query, slot) pairs, the group
+// being consecutive chunks of chunk_rows query rows from row0: the key of the
+// pair in chunk c is c (nkeys + 1) + (b N + t) for a valid index t, and
+// c (nkeys + 1) + nkeys (sorted after the chunk's keys, never reduced)
+// otherwise.  One sort then orders the pairs by chunk, then key, then pair id.
 __global__ void sparse_attn_bwd_pairs_kernel(const void* idx, int idx64, int64_t isb, int64_t iss, int64_t isk,
-                                             int S, int N, int K, int64_t row0, int64_t n, uint32_t sentinel,
-                                             const int32_t* row_len, int64_t rlsb, int64_t rlss, uint32_t* keys,
-                                             uint32_t* vals) {
+                                             int S, int N, int K, int64_t row0, int64_t n, uint32_t nkeys,
+                                             int64_t chunk_rows, const int32_t* row_len, int64_t rlsb, int64_t rlss,
+                                             uint32_t* keys, uint32_t* vals) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n) return;
   const int64_t lrow = p / K;
@@ -799,7 +815,8 @@ __global__ void sparse_attn_bwd_pairs_kernel(const void* idx, int idx64, int64_t
   const int64_t off = b * isb + s * iss + j * isk;
   const int64_t raw = idx64 ? static_cast<const int64_t*>(idx)[off] : static_cast<int64_t>(static_cast<const int32_t*>(idx)[off]);
   const bool in_row = !row_len || j < row_len[b * rlsb + s * rlss];
-  keys[p] = (in_row && raw >= 0 && raw < N) ? static_cast<uint32_t>(b * N + raw) : sentinel;
+  const uint32_t key = (in_row && raw >= 0 && raw < N) ? static_cast<uint32_t>(b * N + raw) : nkeys;
+  keys[p] = static_cast<uint32_t>(lrow / chunk_rows) * (nkeys + 1u) + key;
   vals[p] = static_cast<uint32_t>(p);
 }
 
@@ -809,15 +826,17 @@ __global__ void sparse_attn_bwd_fill_kernel(int32_t* dst, int64_t n, int32_t v) 
     dst[i] = v;
 }
 
-// Each key's run [seg_lo, seg_hi) in the sorted pair list (keys without pairs
-// keep the empty run 0, 0 from the fill).
+// Each (chunk c, key k) run [seg_lo, seg_hi) in the sorted pair list, stored
+// at c nkeys + k (keys without pairs keep the empty run 0, 0 from the fill).
 __global__ void sparse_attn_bwd_segments_kernel(const uint32_t* sk, int64_t n, uint32_t nkeys, int32_t* lo, int32_t* hi) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n) return;
-  const uint32_t k = sk[p];
+  const uint32_t key = sk[p];
+  const uint32_t c = key / (nkeys + 1u), k = key % (nkeys + 1u);
   if (k >= nkeys) return;
-  if (p == 0 || sk[p - 1] != k) lo[k] = static_cast<int32_t>(p);
-  if (p == n - 1 || sk[p + 1] != k) hi[k] = static_cast<int32_t>(p + 1);
+  const int64_t at = static_cast<int64_t>(c) * nkeys + k;
+  if (p == 0 || sk[p - 1] != key) lo[at] = static_cast<int32_t>(p);
+  if (p == n - 1 || sk[p + 1] != key) hi[at] = static_cast<int32_t>(p + 1);
 }
 
 // dsink[h] = sum over rows of the per-row terms, in a fixed order.
@@ -851,17 +870,24 @@ __global__ void sparse_attn_bwd_zero_dkv_kernel(uint16_t* dkv, int64_t dsb, int6
 static size_t bwd_align(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 struct BwdPlan {
-  int64_t rows;  // query rows per chunk
+  int64_t rows;   // query rows per chunk
+  int64_t group;  // chunks per sort group (their pairs are sorted by one radix sort)
+  unsigned end_bit;
   size_t dsink_rows, acc, seg_lo, seg_hi, coef, prow, kin, kout, vin, vout, tmp, tmp_bytes, total;
 };
 
-static unsigned bwd_end_bit(int64_t nkeys) {
+static unsigned bwd_end_bit(int64_t max_key) {
   unsigned bits = 1;
-  while ((int64_t{1} << bits) <= nkeys) ++bits;  // keys 0 .. nkeys (sentinel included)
+  while ((int64_t{1} << bits) <= max_key) ++bits;  // keys 0 .. max_key
   return bits;
 }
 
-static int bwd_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64_t K, int64_t rows, BwdPlan* p) {
+// Workspace layout for chunks of `rows` query rows sorted `group` chunks at a
+// time.  The sort's inputs and its temporary storage share one region with
+// the chunk's coefficient tiles and dkv rows: a group is sorted before its
+// first chunk runs, after the previous group's last chunk has finished.
+static int bwd_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64_t K, int64_t rows, int64_t group,
+                    BwdPlan* p) {
   const int64_t HG = (H + 63) / 64;
   const int64_t ntiles = N > 0 ? (K + kAttnTK - 1) / kAttnTK : 0;
   const int64_t nkeys = B * N;
@@ -874,57 +900,75 @@ static int bwd_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64
     return at;
   };
   p->rows = rows;
+  p->group = group;
+  p->end_bit = bwd_end_bit(group * (nkeys + 1) - 1);
   p->dsink_rows = take(static_cast<size_t>(total_rows) * 64 * HG * 4);
   p->acc = take(chunked ? static_cast<size_t>(nkeys) * D * 4 : 0);
-  p->seg_lo = take(static_cast<size_t>(nkeys) * 4);
-  p->seg_hi = take(static_cast<size_t>(nkeys) * 4);
-  const size_t npairs = ntiles > 0 ? static_cast<size_t>(rows) * K : 0;
+  const size_t npairs = ntiles > 0 ? static_cast<size_t>(rows) * group * K : 0;
+  p->seg_lo = take(static_cast<size_t>(nkeys) * group * 4);
+  p->seg_hi = take(static_cast<size_t>(nkeys) * group * 4);
+  p->kout = take(npairs * 4);
+  p->vout = take(npairs * 4);
+  const size_t shared = off;
   p->coef = take(static_cast<size_t>(rows) * HG * ntiles * kCoefTile * 2);
   p->prow = take(static_cast<size_t>(rows) * HG * ntiles * kAttnTK * D * 2);
+  const size_t chunk_end = off;
+  off = shared;
   p->kin = take(npairs * 4);
-  p->kout = take(npairs * 4);
   p->vin = take(npairs * 4);
-  p->vout = take(npairs * 4);
   size_t tmp = 0;
   if (npairs > 0) {
     const hipError_t e = rocprim::radix_sort_pairs(nullptr, tmp, static_cast<uint32_t*>(nullptr),
                                                    static_cast<uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
-                                                   static_cast<uint32_t*>(nullptr), static_cast<size_t>(npairs), 0u,
-                                                   bwd_end_bit(nkeys), static_cast<hipStream_t>(0));
+                                                   static_cast<uint32_t*>(nullptr), npairs, 0u, p->end_bit,
+                                                   static_cast<hipStream_t>(0));
     if (e != hipSuccess) return set_error(SI_ERR_LAUNCH, std::string("radix sort size query: ") + hipGetErrorString(e));
   }
   p->tmp_bytes = tmp;
   p->tmp = take(tmp);
-  p->total = off;
+  p->total = off > chunk_end ? off : chunk_end;
   return SI_OK;
 }
 
-// Largest chunk (query rows) whose plan fits `bytes`; 0 when even one row does not.
-// A chunk also keeps its (query, slot) pairs and its grid (rows x head groups)
-// inside int32: sort keys, payloads and segment bounds are 32-bit.
+// Largest chunk (query rows) whose plan fits `bytes`; 0 when even one row does
+// not.  A chunk and a sort group keep their (query, slot) pairs and a chunk its
+// grid (rows x head groups) inside int32, and a group's sort keys inside 32
+// bits.  The sort groups take up to a quarter of the budget (pairs and segment
+// bounds), so that a small workspace is not paid for with one radix sort (a
+// few kernels of fixed cost) per chunk.
 static int bwd_rows_for(int64_t B, int64_t S, int64_t H, int64_t D, int64_t N, int64_t K, size_t bytes, BwdPlan* out) {
   const int64_t HG = (H + 63) / 64;
+  const int64_t nkeys = B * N;
   int64_t total = B * S;
   BwdPlan p{};
-  if (total <= 0) return bwd_plan(B, S, H, D, N, K, 0, out);
+  if (total <= 0) return bwd_plan(B, S, H, D, N, K, 0, 1, out);
   const int64_t kLim = 0x7fffffff;
-  int64_t cap = kLim / (K > 0 ? K : 1);
+  const int64_t kpairs = K > 0 ? K : 1;
+  int64_t cap = kLim / kpairs;
   if (kLim / HG < cap) cap = kLim / HG;
   if (total > cap) total = cap;
-  int rc = bwd_plan(B, S, H, D, N, K, total, &p);
+  int rc = bwd_plan(B, S, H, D, N, K, total, 1, &p);
   if (rc) return rc;
-  if (p.total <= bytes) {
+  if (p.total <= bytes && total == B * S) {
     *out = p;
     return SI_OK;
   }
-  int64_t lo = 0, hi = total;  // plan(lo) fits (lo = 0: nothing fits yet), plan(hi) does not
+  auto group_for = [&](int64_t rows) {
+    const int64_t chunks = (B * S + rows - 1) / rows;
+    int64_t g = static_cast<int64_t>(bytes / 4) / (rows * kpairs * 8 + nkeys * 8 + 1);
+    if (g > chunks) g = chunks;
+    if (g > kLim / (rows * kpairs)) g = kLim / (rows * kpairs);
+    if (g > (int64_t{1} << 32) / (nkeys + 1)) g = (int64_t{1} << 32) / (nkeys + 1);
+    return g < 1 ? int64_t{1} : g;
+  };
+  int64_t lo = 0, hi = total + 1;  // plan(lo) fits (lo = 0: nothing fits yet), plan(hi) does not
   while (hi - lo > 1) {
     const int64_t mid = lo + (hi - lo) / 2;
-    rc = bwd_plan(B, S, H, D, N, K, mid, &p);
+    rc = bwd_plan(B, S, H, D, N, K, mid, group_for(mid), &p);
     if (rc) return rc;
     if (p.total <= bytes) lo = mid; else hi = mid;
   }
-  return bwd_plan(B, S, H, D, N, K, lo, out);
+  return bwd_plan(B, S, H, D, N, K, lo, lo > 0 ? group_for(lo) : 1, out);
 }
 
 template <int D, bool F16>
@@ -940,7 +984,6 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
   uint32_t* vout = reinterpret_cast<uint32_t*>(ws + pl.vout);
   int32_t* seg_lo = reinterpret_cast<int32_t*>(ws + pl.seg_lo);
   int32_t* seg_hi = reinterpret_cast<int32_t*>(ws + pl.seg_hi);
-  const unsigned end_bit = bwd_end_bit(nkeys);
   int rc;
   // No (row, key) pair contributes when there are no key tiles or no query
   // rows: dkv is all zeros and the chunk loop below never writes it.
@@ -951,57 +994,68 @@ static int launch_bwd(AttnBwdArgs a, const BwdPlan& pl, char* ws, int64_t total_
                        dkvsb, dkvsn, a.N, D, tot);
     if ((rc = check_launch("sparse_attn_bwd_zero_dkv_kernel"))) return rc;
   }
-  for (int64_t row0 = 0; row0 < total_rows; row0 += pl.rows) {
-    const int64_t nr = total_rows - row0 < pl.rows ? total_rows - row0 : pl.rows;
-    a.row0 = row0;
-    a.nrows = static_cast<int>(nr);
-    const unsigned grid = static_cast<unsigned>(nr * a.HG);
-    if (a.idx64)
-      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, true, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, false, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
-    if ((rc = check_launch("sparse_attn_bwd_rows_kernel"))) return rc;
-    if (a.ntiles == 0) continue;
-    const int64_t npairs = nr * a.K;
-    const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
-    hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, a.idx, a.idx64, a.isb, a.iss,
-                       a.isk, a.S, a.N, a.K, row0, npairs, static_cast<uint32_t>(nkeys), a.row_len, a.rlsb, a.rlss,
-                       kin, vin);
-    if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
-    size_t tmp_bytes = pl.tmp_bytes;
-    const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,
-                                                   static_cast<size_t>(npairs), 0u, end_bit, st);
-    if (e != hipSuccess) return set_error(SI_ERR_LAUNCH, std::string("radix sort: ") + hipGetErrorString(e));
-    const int64_t fblocks = (2 * nkeys + 255) / 256 < 65536 ? (2 * nkeys + 255) / 256 : 65536;
-    // seg_lo and seg_hi are adjacent 256-byte-aligned runs: clear each
-    hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_lo,
-                       nkeys, 0);
-    hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_hi,
-                       nkeys, 0);
-    if ((rc = check_launch("sparse_attn_bwd_fill_kernel"))) return rc;
-    hipLaunchKernelGGL(sparse_attn_bwd_segments_kernel, dim3(pblocks), dim3(256), 0, st, kout, npairs,
-                       static_cast<uint32_t>(nkeys), seg_lo, seg_hi);
-    if ((rc = check_launch("sparse_attn_bwd_segments_kernel"))) return rc;
-    hipLaunchKernelGGL((sparse_attn_bwd_dkv_rows_kernel<D, F16>), dim3(grid), dim3(kRowsThreads), 0, st, a);
-    if ((rc = check_launch("sparse_attn_bwd_dkv_rows_kernel"))) return rc;
-    DkvReduceArgs r{};
-    r.pair = vout;
-    r.seg_lo = seg_lo;
-    r.seg_hi = seg_hi;
-    r.prow = a.prow;
-    r.acc = reinterpret_cast<float*>(ws + pl.acc);
-    r.dkv = dkv;
-    r.dsb = dkvsb;
-    r.dsn = dkvsn;
-    r.K = a.K;
-    r.KP = a.ntiles * kAttnTK;
-    r.HG = a.HG;
-    r.N = a.N;
-    r.first = row0 == 0;
-    r.last = row0 + nr >= total_rows;
-    hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D, F16>), dim3(static_cast<unsigned>(nkeys)),
-                       dim3(ReduceShape<D>::NT), 0, st, r);
-    if ((rc = check_launch("sparse_attn_bwd_dkv_reduce_kernel"))) return rc;
+  const int64_t grows_max = pl.rows * pl.group;
+  for (int64_t g0 = 0; g0 < total_rows; g0 += grows_max) {
+    const int64_t grows = total_rows - g0 < grows_max ? total_rows - g0 : grows_max;
+    const int64_t gchunks = (grows + pl.rows - 1) / pl.rows;
+    if (a.ntiles > 0) {
+      // the group's pairs, sorted by (chunk, key, pair id), and each
+      // (chunk, key)'s run in that order
+      const int64_t npairs = grows * a.K;
+      const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
+      hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, a.idx, a.idx64, a.isb, a.iss,
+                         a.isk, a.S, a.N, a.K, g0, npairs, static_cast<uint32_t>(nkeys), pl.rows, a.row_len, a.rlsb,
+                         a.rlss, kin, vin);
+      if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
+      size_t tmp_bytes = pl.tmp_bytes;
+      const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,
+                                                     static_cast<size_t>(npairs), 0u, pl.end_bit, st);
+      if (e != hipSuccess) return set_error(SI_ERR_LAUNCH, std::string("radix sort: ") + hipGetErrorString(e));
+      const int64_t nseg = gchunks * nkeys;
+      const int64_t fblocks = (nseg + 255) / 256 < 65536 ? (nseg + 255) / 256 : 65536;
+      hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_lo,
+                         nseg, 0);
+      hipLaunchKernelGGL(sparse_attn_bwd_fill_kernel, dim3(static_cast<unsigned>(fblocks)), dim3(256), 0, st, seg_hi,
+                         nseg, 0);
+      if ((rc = check_launch("sparse_attn_bwd_fill_kernel"))) return rc;
+      hipLaunchKernelGGL(sparse_attn_bwd_segments_kernel, dim3(pblocks), dim3(256), 0, st, kout, npairs,
+                         static_cast<uint32_t>(nkeys), seg_lo, seg_hi);
+      if ((rc = check_launch("sparse_attn_bwd_segments_kernel"))) return rc;
+    }
+    for (int64_t c = 0; c < gchunks; ++c) {
+      const int64_t row0 = g0 + c * pl.rows;
+      const int64_t nr = total_rows - row0 < pl.rows ? total_rows - row0 : pl.rows;
+      a.row0 = row0;
+      a.nrows = static_cast<int>(nr);
+      const unsigned grid = static_cast<unsigned>(nr * a.HG);
+      if (a.idx64)
+        hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, true, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((sparse_attn_bwd_rows_kernel<D, false, F16>), dim3(grid), dim3(kBwdThreads), 0, st, a);
+      if ((rc = check_launch("sparse_attn_bwd_rows_kernel"))) return rc;
+      if (a.ntiles == 0) continue;
+      hipLaunchKernelGGL((sparse_attn_bwd_dkv_rows_kernel<D, F16>), dim3(grid), dim3(kRowsThreads), 0, st, a);
+      if ((rc = check_launch("sparse_attn_bwd_dkv_rows_kernel"))) return rc;
+      DkvReduceArgs r{};
+      r.pair = vout;
+      r.seg_lo = seg_lo + c * nkeys;
+      r.seg_hi = seg_hi + c * nkeys;
+      r.prow = a.prow;
+      r.acc = reinterpret_cast<float*>(ws + pl.acc);
+      r.dkv = dkv;
+      r.dsb = dkvsb;
+      r.dsn = dkvsn;
+      r.prow0 = c * pl.rows;
+      r.K = a.K;
+      r.KP = a.ntiles * kAttnTK;
+      r.HG = a.HG;
+      r.N = a.N;
+      r.first = row0 == 0;
+      r.last = row0 + nr >= total_rows;
+      hipLaunchKernelGGL((sparse_attn_bwd_dkv_reduce_kernel<D, F16>), dim3(static_cast<unsigned>(nkeys)),
+                         dim3(ReduceShape<D>::NT), 0, st, r);
+      if ((rc = check_launch("sparse_attn_bwd_dkv_reduce_kernel"))) return rc;
+    }
   }
   hipLaunchKernelGGL(sparse_attn_bwd_dsink_kernel, dim3(static_cast<unsigned>(a.H)), dim3(256), 0, st, a.dsink_rows,
                      total_rows, 64 * a.HG, dsink);
@@ -1085,7 +1139,7 @@ extern "C" int64_t si_sparse_attn_bwd_workspace_bytes(int64_t B, int64_t S, int6
   int rc = bwd_rows_for(B, S, H, D, N_kv, K, static_cast<size_t>(max_bytes), &p);
   if (rc) return -1;
   if (p.rows == 0 && B * S > 0) {  // not even one row fits: report the one-row need
-    rc = bwd_plan(B, S, H, D, N_kv, K, 1, &p);
+    rc = bwd_plan(B, S, H, D, N_kv, K, 1, 1, &p);
     if (rc) return -1;
   }
   return static_cast<int64_t>(p.total);
@@ -1249,8 +1303,8 @@ extern "C" int si_build_inverted_topk(const void* topk_idxs, int idx_is_i64, con
     const unsigned pblocks = static_cast<unsigned>((npairs + 255) / 256);
     hipLaunchKernelGGL(sparse_attn_bwd_pairs_kernel, dim3(pblocks), dim3(256), 0, st, topk_idxs, idx_is_i64 ? 1 : 0,
                        idx_strides[0], idx_strides[1], idx_strides[2], static_cast<int>(S), static_cast<int>(n_kv),
-                       static_cast<int>(K), int64_t{0}, npairs, static_cast<uint32_t>(nkeys), nullptr, int64_t{0},
-                       int64_t{0}, kin, vin);
+                       static_cast<int>(K), int64_t{0}, npairs, static_cast<uint32_t>(nkeys), B * S, nullptr,
+                       int64_t{0}, int64_t{0}, kin, vin);
     if ((rc = check_launch("sparse_attn_bwd_pairs_kernel"))) return rc;
     size_t tmp_bytes = pl.tmp_bytes;
     const hipError_t e = rocprim::radix_sort_pairs(ws + pl.tmp, tmp_bytes, kin, kout, vin, vout,
