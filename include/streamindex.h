@@ -152,7 +152,7 @@ int si_sparse_attn_fwd_ragged(const void* q, const int64_t* q_strides, const voi
  * [0, N_kv) select rows of kv [B,N_kv,D], indices in [N_kv, N_kv + N_kv2)
  * rows of kv2 [B,N_kv2,D] (same element type, strides kv2_strides[3]).
  * Equal to si_sparse_attn_fwd_ragged over their concatenation along N.
- * topk_idxs is int32; each tensor's batch must be below 32 GiB.  Replaces
+ * topk_idxs is int32; N_kv + N_kv2 must fit in int32.  Replaces
  * the torch.cat([kv, kv_compressed]) that feeds sparse_attn_fwd in
  * flash_sparse/csa.py:197-205 and flash_sparse/hca.py:85-95.
  */

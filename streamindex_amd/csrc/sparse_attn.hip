@@ -103,9 +103,12 @@ constexpr int attn_rows_per_workgroup() {
   return D >= 512 ? 8 : 1;
 }
 
-// With KV2 a published row offset carries the tensor in bit 31 (set: the
-// second KV tensor); each tensor's batch holds at most 2^31 16-byte units.
-constexpr uint32_t kKv2Bit = 0x80000000u;
+// Published KV row offsets: 16-byte units from the batch's first KV row
+// (32 bits) with one KV tensor; with two (KV2) signed byte offsets from the
+// first tensor's batch base (64 bits), so that a key of either tensor costs
+// one 64-bit add per copy, with no per-copy choice between two bases.
+template <bool KV2>
+using AttnRowOff = std::conditional_t<KV2, int64_t, uint32_t>;
 
 template <int D, bool IDX64, bool F16, bool KV2>
 __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAttnArgs a) {
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   __shared__ int live_lds[2];  // tile has at least one valid key (published with alpha)
   __shared__ float scale_lds[64];
   __shared__ __attribute__((aligned(16))) float bias_lds[kAttnRing][kAttnTK];  // 0: key used, -inf: masked
-  __shared__ uint32_t rowoff_lds[kAttnRing][kAttnTK];    // offset of the key's KV row, 16-byte units
+  __shared__ AttnRowOff<KV2> rowoff_lds[kAttnRing][kAttnTK];  // offset of the key's KV row
   __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[2 * kAttnRing][2 * kAttnTK];  // raw index words
 
   const int lane = threadIdx.x & 63;
@@ -193,11 +196,11 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       // ---- KV gather (issued by the producers, which wait at the tile barrier
       // for the P.V waves otherwise) -------------------------------------------
       const char* kvb = reinterpret_cast<const char*>(a.kv + b * a.kvsb);
-      const char* kvb2 = KV2 ? reinterpret_cast<const char*>(a.kv2 + b * a.kv2sb) : kvb;
       // Gather of tile `t` into its ring slot: LDS slot e (16 bytes at byte 16e)
       // holds chunk (e % CPR) ^ f(key) of key e / CPR.  This thread's key and
       // chunk (in 16-byte units) per copy are fixed, computed once; a copy's
-      // source is kv + 16 (rowoff16[key] + dcoff).
+      // source is kv + 16 (rowoff16[key] + dcoff), or kv + rowoff[key] + 16 dcoff
+      // with two KV tensors.
       int dkey[SH::LPT], dcoff[SH::LPT];
   #pragma unroll
       for (int i = 0; i < SH::LPT; ++i) {
@@ -205,12 +208,17 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         dkey[i] = e / SH::CPR;
         dcoff[i] = (e % SH::CPR) ^ kv_swz<D>(dkey[i]);
       }
-      uint32_t roff[SH::LPT];  // copy sources of the tile being gathered
-      auto read_roff = [&](int t, uint32_t (&dst)[SH::LPT]) {
+      using RowOff = AttnRowOff<KV2>;
+      RowOff roff[SH::LPT];  // copy sources of the tile being gathered
+      auto read_roff = [&](int t, RowOff (&dst)[SH::LPT]) {
         const int slot = t % kAttnRing;
   #pragma unroll
-        for (int i = 0; i < SH::LPT; ++i)
-          dst[i] = (i * SH::NT + wave * 64 < SH::CH) ? rowoff_lds[slot][dkey[i]] + dcoff[i] : 0u;
+        for (int i = 0; i < SH::LPT; ++i) {
+          if (i * SH::NT + wave * 64 < SH::CH)
+            dst[i] = rowoff_lds[slot][dkey[i]] + (KV2 ? 16 * dcoff[i] : dcoff[i]);
+          else
+            dst[i] = 0;
+        }
       };
       // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
       // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
@@ -222,8 +230,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         // drop the host launch stubs of later instantiations)
         const uint16_t* src;
         if constexpr (KV2) {
-          const char* base = (roff[i] & kKv2Bit) ? kvb2 : kvb;
-          src = reinterpret_cast<const uint16_t*>(base + (static_cast<uint64_t>(roff[i] & ~kKv2Bit) << 4));
+          src = reinterpret_cast<const uint16_t*>(kvb + roff[i]);
         } else {
           src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
         }
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
         attn_tile_barrier();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
         attn_tile_barrier();  // indices of tile 4 published
-        uint32_t roff_nx[SH::LPT];  // copy sources of tile it+4
+        RowOff roff_nx[SH::LPT];  // copy sources of tile it+4
         for (int it = 0; it < ntiles; ++it) {
           const bool issue = it + 3 < ntiles;
           // tracked LDS reads first, then the copies of tile it+3 into the slot
@@ -462,10 +469,14 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
           const bool ok = j < klen && raw >= 0 && raw < a.N;
           bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
           if constexpr (KV2) {
+            // byte offsets from the first tensor's batch base; a masked key
+            // reads the first row of a tensor that has rows
+            const int64_t kv2_delta = reinterpret_cast<const char*>(a.kv2 + b * a.kv2sb) -
+                                      reinterpret_cast<const char*>(a.kv + b * a.kvsb);
             const bool second = raw >= a.N1;
-            rowoff_lds[slot][lane] = !ok ? 0u
-                                     : second ? (kKv2Bit | static_cast<uint32_t>((raw - a.N1) * (a.kv2sn / 8)))
-                                              : static_cast<uint32_t>(raw * (a.kvsn / 8));
+            rowoff_lds[slot][lane] = !ok ? (a.N1 > 0 ? int64_t{0} : kv2_delta)
+                                     : second ? kv2_delta + (raw - a.N1) * a.kv2sn * 2
+                                              : raw * a.kvsn * 2;
           } else {
             rowoff_lds[slot][lane] = static_cast<uint32_t>((ok ? raw : 0) * (a.kvsn / 8));
           }
@@ -664,11 +675,10 @@ static int sparse_attn_fwd_entry(const void* q, const int64_t* q_strides, const 
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kv)) & 15)
     return set_error(SI_ERR_INVALID, "q/kv must be 16-byte aligned");
   if (reinterpret_cast<uintptr_t>(o) & 15) return set_error(SI_ERR_INVALID, "o must be 16-byte aligned");
-  // KV row offsets are kept in 32 bits, in 16-byte units, inside one batch
-  // (31 bits per tensor with a second KV tensor).
-  const int off_bits = kv2 ? 31 : 32;
-  if (N_kv > 0 && ((N_kv - 1) * kv_strides[1] + D) / 8 >= (int64_t{1} << off_bits))
-    return set_error(SI_ERR_UNSUPPORTED, kv2 ? "kv batch larger than 32 GiB" : "kv batch larger than 64 GiB");
+  // With one KV tensor its row offsets are kept in 32 bits, in 16-byte units,
+  // inside one batch (two tensors use 64-bit byte offsets).
+  if (!kv2 && N_kv > 0 && ((N_kv - 1) * kv_strides[1] + D) / 8 >= (int64_t{1} << 32))
+    return set_error(SI_ERR_UNSUPPORTED, "kv batch larger than 64 GiB");
   if (kv2) {
     if (!kv2_strides) return set_error(SI_ERR_INVALID, "null stride argument");
     if (N_kv2 < 0) return set_error(SI_ERR_INVALID, "bad dimension");
@@ -676,8 +686,6 @@ static int sparse_attn_fwd_entry(const void* q, const int64_t* q_strides, const 
     if (idx_is_i64) return set_error(SI_ERR_UNSUPPORTED, "two KV tensors take int32 indices");
     if (kv2_strides[2] != 1 || (kv2_strides[0] | kv2_strides[1]) % 8 || (reinterpret_cast<uintptr_t>(kv2) & 15))
       return set_error(SI_ERR_INVALID, "kv2 needs a contiguous last dimension, 16-byte rows and alignment");
-    if (N_kv2 > 0 && ((N_kv2 - 1) * kv2_strides[1] + D) / 8 >= (int64_t{1} << 31))
-      return set_error(SI_ERR_UNSUPPORTED, "kv2 batch larger than 32 GiB");
   }
   SparseAttnArgs a{};
   if (kv2 && N_kv2 > 0) {
