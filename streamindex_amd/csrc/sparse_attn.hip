@@ -123,6 +123,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   __shared__ int live_lds[2];  // tile has at least one valid key (published with alpha)
   __shared__ float scale_lds[64];
   __shared__ __attribute__((aligned(16))) float bias_lds[kAttnRing][kAttnTK];  // 0: key used, -inf: masked
+  __shared__ int tlive_lds[kAttnRing];  // the tile has at least one valid key (published with the biases)
   __shared__ AttnRowOff<KV2> rowoff_lds[kAttnRing][kAttnTK];  // offset of the key's KV row
   __shared__ __attribute__((aligned(16))) uint32_t idxraw_lds[2 * kAttnRing][2 * kAttnTK];  // raw index words
 
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       };
       // Copy i of tile t (one 64-lane group of 16-byte slots); every 64-slot
       // group lies wholly inside or wholly outside the tile (CH % 64 == 0).
-      auto dma = [&](int t, auto IC) {
+      auto dma = [&](int t, const RowOff (&ro)[SH::LPT], auto IC) {
         constexpr int i = decltype(IC)::value;
         const int e0 = i * SH::NT + wave * 64;
         char* dst = kv_lds + (t % kAttnRing) * SH::TILE + e0 * 16;
@@ -230,9 +231,9 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         // drop the host launch stubs of later instantiations)
         const uint16_t* src;
         if constexpr (KV2) {
-          src = reinterpret_cast<const uint16_t*>(kvb + roff[i]);
+          src = reinterpret_cast<const uint16_t*>(kvb + ro[i]);
         } else {
-          src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(roff[i]) << 4));
+          src = reinterpret_cast<const uint16_t*>(kvb + (static_cast<uint64_t>(ro[i]) << 4));
         }
         if constexpr (SH::CH % SH::NT == 0 || i + 1 < SH::LPT) {
           __builtin_amdgcn_global_load_lds(src, (lds_void_t*)dst, 16, 0, 0);
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       // The copies of tile `src` (its row offsets) into the ring slot of tile `dst`.
       auto issue_tile_from = [&](int src, int dst) {
         read_roff(src, roff);
-        attn_static_for<0, SH::LPT>([&](auto IC) { dma(dst, IC); });
+        attn_static_for<0, SH::LPT>([&](auto IC) { dma(dst, roff, IC); });
       };
 
 
@@ -339,16 +340,15 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         bias[0] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][4 * g]);
         bias[1] = *reinterpret_cast<const f32x4*>(&bias_lds[t % kAttnRing][16 + 4 * g]);
       };
-      // Whether any key of the tile is valid (wave-uniform): the four lane
-      // groups' biases cover all 32 keys.  An all-masked tile needs no S^T (its
-      // scores are 0 + bias = -inf either way) and no P.V (P = 0).
-      auto tile_live = [&](const f32x4 (&bias)[2]) {
-        bool any = false;
-  #pragma unroll
-        for (int r = 0; r < 4; ++r) any |= (bias[0][r] == 0.f) | (bias[1][r] == 0.f);
-        return __builtin_amdgcn_ballot_w64(any) != 0;
-      };
+      // Whether any key of tile t is valid, as the index wave published it
+      // with the biases (read with them, made wave-uniform at its use).  An
+      // all-masked tile needs no S^T (its scores are finite + bias = -inf
+      // either way, so the scores of the last computed tile serve) and no
+      // P.V (P = 0).
+      auto read_live = [&](int t) { return tlive_lds[t % kAttnRing]; };
+      auto is_live = [&](int v) { return __builtin_amdgcn_readfirstlane(v) != 0; };
       const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 st[2] = {zero4, zero4};  // S^T accumulators (kept across tiles, see above; one KV tensor)
 
       if (ntiles > 0) {
         // (prologue barriers without a release fence, like the tile barrier: a
@@ -365,44 +365,77 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         // tile 0 (and every Q load) landed; the copies of tiles 1 and 2 may still be in flight
         __builtin_amdgcn_s_waitcnt(vm_lgkm0(2 * SH::LPT));
         attn_tile_barrier();  // tile 0 landed
-        f32x4 bias_cur[2];
+        // Per-tile state alternates between two register sets (the loop runs
+        // two tiles per trip), so nothing is copied from one tile to the next.
+        f32x4 bias_a[2], bias_b[2];
+        int live_a, live_b;
+        RowOff roff_b[SH::LPT];
         {
-          f32x4 bias[2], st[2] = {zero4, zero4};
+          f32x4 bias[2];
           read_bias(0, bias);
-          read_bias(1, bias_cur);
+          const int live0 = read_live(0);
+          read_bias(1, bias_a);
+          live_a = read_live(1);
           read_roff(3, roff);
-          const bool live = tile_live(bias);
-          if (live) qk(0, st);
-          softmax_store(0, softmax(st, bias), live);
+          const bool live = is_live(live0);
+          f32x4 st0[2] = {zero4, zero4};
+          if (live) qk(0, st0);
+          softmax_store(0, softmax(st0, bias), live);
+          if constexpr (!KV2) {
+            st[0] = st0[0];
+            st[1] = st0[1];
+          }
         }
         // tile 1 landed; the copies of tile 2 may still be in flight
         __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
         attn_tile_barrier();  // tile 1 landed; P^T of tile 0 published; tile 0's biases and offsets read
         attn_tile_barrier();  // indices of tile 4 published
-        RowOff roff_nx[SH::LPT];  // copy sources of tile it+4
-        for (int it = 0; it < ntiles; ++it) {
+        // Iteration it with the state of tile it+1 in (bias_c, live_c), the
+        // copy sources of tile it+3 in ro_c; it reads those of tiles it+2 and
+        // it+4 into the other set.
+        auto iteration = [&](int it, f32x4 (&bias_c)[2], int& live_c, f32x4 (&bias_n)[2], int& live_n,
+                             const RowOff (&ro_c)[SH::LPT], RowOff (&ro_n)[SH::LPT]) {
           const bool issue = it + 3 < ntiles;
           // tracked LDS reads first, then the copies of tile it+3 into the slot
           // of tile it-1 (finished by every wave in iteration it-1)
-          f32x4 bias_nx[2];
-          read_bias(it + 2, bias_nx);    // slots read are always inside the arrays
-          read_roff(it + 4, roff_nx);
-          if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, IC); });
+          read_bias(it + 2, bias_n);    // slots read are always inside the arrays
+          live_n = read_live(it + 2);
+          read_roff(it + 4, ro_n);
+          if (issue) attn_static_for<0, SH::LPT>([&](auto IC) { dma(it + 3, ro_c, IC); });
           if (it + 1 < ntiles) {
-            f32x4 st[2] = {zero4, zero4};
-            const bool live = tile_live(bias_cur);
-            if (live) qk(it + 1, st);
-            softmax_store(it + 1, softmax(st, bias_cur), live);
+            const bool live = is_live(live_c);
+            if constexpr (KV2) {
+              // (zeroed per tile: this variant has no registers to spare)
+              f32x4 stl[2] = {zero4, zero4};
+              if (live) qk(it + 1, stl);
+              softmax_store(it + 1, softmax(stl, bias_c), live);
+            } else {
+              if (live) qk(it + 1, st);
+              softmax_store(it + 1, softmax(st, bias_c), live);
+            }
           }
-          bias_cur[0] = bias_nx[0];
-          bias_cur[1] = bias_nx[1];
-  #pragma unroll
-          for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_nx[i];
           // the copies of tile it+2 (issued one iteration ago) landed; those of
           // tile it+3 stay in flight across the barrier
           if (issue) __builtin_amdgcn_s_waitcnt(vm_lgkm0(SH::LPT));
           else __builtin_amdgcn_s_waitcnt(vm_lgkm0(0));
           attn_tile_barrier();
+        };
+        if constexpr (KV2) {
+          // (64-bit copy sources: two register sets of them would not fit
+          // beside the rest, so this variant copies them forward per tile)
+          for (int it = 0; it < ntiles; ++it) {
+            iteration(it, bias_a, live_a, bias_b, live_b, roff, roff_b);
+            bias_a[0] = bias_b[0];
+            bias_a[1] = bias_b[1];
+            live_a = live_b;
+  #pragma unroll
+            for (int i = 0; i < SH::LPT; ++i) roff[i] = roff_b[i];
+          }
+        } else {
+          for (int it = 0; it < ntiles; it += 2) {
+            iteration(it, bias_a, live_a, bias_b, live_b, roff, roff_b);
+            if (it + 1 < ntiles) iteration(it + 1, bias_b, live_b, bias_a, live_a, roff_b, roff);
+          }
         }
       }
 
@@ -461,12 +494,15 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
       auto store_idx = [&](int t) {
         const int slot = t % kAttnRing;
         const int rslot = t % (2 * kAttnRing);
+        const int ln = lane < kAttnTK ? lane : 0;
+        const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * ln + 1]) << 32) |
+                                                         idxraw_lds[rslot][2 * ln])
+                                  : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][ln]));
+        const bool ok = lane < kAttnTK && t * kAttnTK + lane < klen && raw >= 0 && raw < a.N;
+        // whether any key of the tile is valid, for the producers
+        const bool live = __builtin_amdgcn_ballot_w64(ok) != 0;
+        if (lane == 0) tlive_lds[slot] = live ? 1 : 0;
         if (lane < kAttnTK) {
-          const int64_t raw = IDX64 ? static_cast<int64_t>((static_cast<uint64_t>(idxraw_lds[rslot][2 * lane + 1]) << 32) |
-                                                           idxraw_lds[rslot][2 * lane])
-                                    : static_cast<int64_t>(static_cast<int32_t>(idxraw_lds[rslot][lane]));
-          const int j = t * kAttnTK + lane;
-          const bool ok = j < klen && raw >= 0 && raw < a.N;
           bias_lds[slot][lane] = ok ? 0.f : -__builtin_inff();
           if constexpr (KV2) {
             // byte offsets from the first tensor's batch base; a masked key
