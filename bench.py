@@ -734,6 +734,10 @@ def main():
                     help="config[3] sparse-attention timing only, on config[1]'s indexer output (for profilers)")
     ap.add_argument("--only-attn-random", action="store_true",
                     help="sparse-attention timing on random causal indices only (for profilers)")
+    ap.add_argument("--idx-order", choices=("given", "sorted"), default="given",
+                    help="with --only-attn: the indexer's order (best score first) or each row sorted by key "
+                         "(descending, -1 last)")
+    ap.add_argument("--idx-int32", action="store_true", help="with --only-attn: int32 instead of int64 indices")
     ap.add_argument("--only-attn-bwd", action="store_true", help="sparse-attention backward timing only (for profilers)")
     ap.add_argument("--bwd-workspace-gib", type=float, default=0.0, metavar="GIB",
                     help="with --only-attn-bwd: cap the backward's workspace at GIB (default: the library's cap)")
@@ -791,6 +795,11 @@ def main():
             ri = run_indexer(65536, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
             idx = ri["idx"]
             del ri
+            if args.idx_order == "sorted":
+                # the same keys per row (the result does not depend on their order)
+                idx = torch.sort(idx, dim=-1, descending=True).values
+            if args.idx_int32:
+                idx = idx.to(torch.int32)
             torch.cuda.empty_cache()
         ra = run_sparse_attn(65536, 16384, 64, 576, 512, args.steps, args.warmup, idx=idx)
         print(json.dumps({"sparse_attn_ms": ra["ms"], "tflops": ra["flops"] / ra["ms"] / 1e9,

@@ -322,6 +322,25 @@ def test_two_kv_tensors(cuda_device, D, H, f16):
     assert torch.equal(torch.cat([g1[1], g1[2]], dim=1), g2[1])
 
 
+def test_two_kv_empty_first(cuda_device):
+    # no rows in the first tensor (its data pointer may be null): every index
+    # selects a row of the second one, masked keys must not read the first;
+    # bit-identical to the one-tensor forward over the second tensor
+    from streamindex_amd import sparse_attn_fwd_kv2
+
+    B, S, H, D, N2, K = 2, 24, 64, 576, 45, 64
+    q, kv2, sink = synth.sparse_attn_inputs(B, S, H, D, N2, seed=411)
+    kv = torch.empty(B, 0, D, dtype=kv2.dtype, device=kv2.device)
+    g = torch.Generator().manual_seed(2)
+    idx = torch.randint(-1, N2 + 4, (B, S, K), generator=g, dtype=torch.int32).cuda()
+    rl = torch.randint(0, K + 1, (B, S), generator=g, dtype=torch.int32).cuda()
+    for row_len in (None, rl):
+        o1, l1 = sparse_attn_fwd_kv2(q, kv, kv2, sink, idx, row_len=row_len)
+        o2, l2 = sparse_attn_fwd(q, kv2, sink, idx, row_len=row_len)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
 def test_two_kv_empty_second(cuda_device):
     # no rows in the second tensor: the one-tensor path; indices past N1 masked
     from streamindex_amd import sparse_attn_fwd_kv2
