@@ -69,15 +69,17 @@ __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 template <int LX>
 __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t x) {
   const int xi = static_cast<int>(x);
+  // (mov_dpp leaves the lanes it does not write undefined, so the compiler
+  // needs no copy of the old value; every lane is written here.)
   if constexpr (LX == 1) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(xi, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
   } else if constexpr (LX == 2) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(xi, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
   } else if constexpr (LX == 4) {
-    const int t = __builtin_amdgcn_update_dpp(xi, xi, 0x114, 0xf, 0xA, false);  // row_shr:4 into banks 1,3
+    const int t = __builtin_amdgcn_mov_dpp(xi, 0x114, 0xf, 0xA, false);  // row_shr:4 into banks 1,3
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(t, xi, 0x104, 0xf, 0x5, false));  // row_shl:4 into 0,2
   } else if constexpr (LX == 8) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(xi, xi, 0x128, 0xf, 0xf, false));  // row_ror:8
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(xi, 0x128, 0xf, 0xf, false));  // row_ror:8
   } else if constexpr (LX == 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
     return __builtin_amdgcn_inverse_ballot_w64(0xFFFF0000FFFF0000ull) ? static_cast<uint32_t>(r[0])
@@ -115,10 +117,10 @@ __device__ __forceinline__ SwapPair permlane32_swap(uint32_t a, uint32_t b) {
 // mirrors; across rows: v_permlane16_swap and v_permlane32_swap.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
   auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
-  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0xB1, 0xf, 0xf, false)));
-  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x4E, 0xf, 0xf, false)));
-  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x141, 0xf, 0xf, false)));
-  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x140, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xf, 0xf, false)));
+  x = mx(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xf, 0xf, false)));
   const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
   x = mx(static_cast<uint32_t>(r16[0]), static_cast<uint32_t>(r16[1]));
   const auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);

@@ -54,9 +54,69 @@ constexpr uint64_t keep_max_lane_mask() {
   return m;
 }
 
+// Half-row (LX = 16) or half-wave (LX = 32) exchange of two registers:
+// v_permlane{16,32}_swap trades the upper LX-lane groups of `a` with the
+// lower ones of `b`, so afterwards every lane holds one partner pair
+// (lane p, lane p + LX): that of `a` in lanes whose LX bit is clear, that of
+// `b` in the others, with the lower lane's value in `a`.  Applying it again
+// restores both registers.
+template <int LX>
+__device__ __forceinline__ void lane_pair_swap(uint32_t& a, uint32_t& b) {
+  if constexpr (LX == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = static_cast<uint32_t>(r[0]);
+    b = static_cast<uint32_t>(r[1]);
+  } else {
+    static_assert(LX == 32, "lane pair distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = static_cast<uint32_t>(r[0]);
+    b = static_cast<uint32_t>(r[1]);
+  }
+}
+
+// After lane_pair_swap<LX>, lanes holding a pair whose block runs descending:
+// the pair's lower lane is l, or l - LX when l's LX bit is set.
+template <int E, int N, int SIZE, int LX>
+constexpr uint64_t pair_desc_lane_mask() {
+  uint64_t m = 0;
+  for (int l = 0; l < kWave; ++l) {
+    const int p = l & ~LX;
+    if (SIZE >= N || ((p * E) & SIZE) == 0) m |= 1ull << l;
+  }
+  return m;
+}
+
 template <int E, int N, int SIZE, int STRIDE>
 __device__ __forceinline__ void bitonic_stage(uint64_t (&v)[E], int lane) {
-  if constexpr (STRIDE >= E) {
+  if constexpr (STRIDE >= E && (STRIDE / E == 16 || STRIDE / E == 32) && E % 2 == 0) {
+    // Registers j and j+1 are exchanged pairwise so that both keys of every
+    // compare-exchange sit in one lane (lower lane's key in x), compared
+    // in-lane, and exchanged back: four swaps per two keys instead of a
+    // copy, a swap and a select per 32-bit half of each key.
+    constexpr int LX = STRIDE / E;
+    constexpr uint64_t DM = pair_desc_lane_mask<E, N, SIZE, LX>();
+#pragma unroll
+    for (int j = 0; j < E; j += 2) {
+      uint32_t xlo = static_cast<uint32_t>(v[j]), xhi = static_cast<uint32_t>(v[j] >> 32);
+      uint32_t ylo = static_cast<uint32_t>(v[j + 1]), yhi = static_cast<uint32_t>(v[j + 1] >> 32);
+      lane_pair_swap<LX>(xlo, ylo);
+      lane_pair_swap<LX>(xhi, yhi);
+      const uint64_t x = (static_cast<uint64_t>(xhi) << 32) | xlo;
+      const uint64_t y = (static_cast<uint64_t>(yhi) << 32) | ylo;
+      // descending pair: the lower lane keeps the larger key (swap when x < y)
+      const uint64_t lt = __builtin_amdgcn_ballot_w64(x < y);
+      const bool sw = __builtin_amdgcn_inverse_ballot_w64(~(lt ^ DM));
+      const uint64_t nx = sw ? y : x, ny = sw ? x : y;
+      xlo = static_cast<uint32_t>(nx);
+      xhi = static_cast<uint32_t>(nx >> 32);
+      ylo = static_cast<uint32_t>(ny);
+      yhi = static_cast<uint32_t>(ny >> 32);
+      lane_pair_swap<LX>(xlo, ylo);
+      lane_pair_swap<LX>(xhi, yhi);
+      v[j] = (static_cast<uint64_t>(xhi) << 32) | xlo;
+      v[j + 1] = (static_cast<uint64_t>(yhi) << 32) | ylo;
+    }
+  } else if constexpr (STRIDE >= E) {
     constexpr int LX = STRIDE / E;
     constexpr uint64_t KM = keep_max_lane_mask<E, N, SIZE, LX>();
     uint64_t o[E];
