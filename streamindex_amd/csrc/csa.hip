@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void score_topk_kernel(ScoreTopkArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (base + u * kWave < lim) {
-        if (sel.needs_compaction()) sel.compact(lane);
+        if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
         const int t = base + u * kWave + lane;
         const uint64_t key = make_key(v[u], static_cast<uint32_t>(t));
         const bool pass = t < lim && v[u] != -__builtin_inff() && key_hi(key) > sel.tau;

@@ -494,7 +494,7 @@ void indexer_topk_kernel(IndexerArgs a) {
     if constexpr (SHARE_COMP) {
       comp_req[(it & 1) * NW + wave] = sel.needs_compaction();
     } else {
-      if (sel.needs_compaction()) sel.compact(lane);
+      if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
     }
     // Tile it+1 must have landed.
     wait_vm_lgkm0<0>();
@@ -509,7 +509,7 @@ void indexer_topk_kernel(IndexerArgs a) {
     if (it < ntiles) tile_step(it, std::integral_constant<int, 0>{});
   }
 
-  if (sel.needs_compaction()) sel.compact(lane);  // room for the pending offer
+  if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);  // room for the pending offer
   if (pend) drain();
 
   if (active) {

@@ -248,7 +248,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
       const bool legal = t < my_lim && mok;
       const uint64_t key = make_key(sum, static_cast<uint32_t>(t));
       sel.offer64(legal && key_hi(key) > sel.tau, key, lane);
-      if (sel.needs_compaction()) sel.compact(lane);
+      if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
     }
     if (more) wait_vm_lgkm0<0>();
     __syncthreads();

@@ -178,7 +178,7 @@ void indexer_topk_split_kernel(IndexerArgs a) {
       const uint64_t key = make_key(tot, static_cast<uint32_t>(t));
       sel.offer64(legal && key_hi(key) > sel.tau, key, lane);
       // one offer per tile: compact before the next one can overflow
-      if (sel.needs_compaction()) sel.compact(lane);
+      if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
     }
     // Tile it+1 landed; the partial scores of this tile have been read.
     wait_vm_lgkm0<0>();

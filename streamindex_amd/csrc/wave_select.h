@@ -225,27 +225,33 @@ struct WaveSelect {
   // compaction keeps to the compaction threshold.
   __device__ __forceinline__ bool wants_compaction() const { return n > (compact_cmax() + C - 2 * kWave) / 2; }
 
-  // Bits of a per-lane count in [0, E].
-  static constexpr int EBITS = E < 16 ? 4 : (E < 32 ? 5 : (E < 64 ? 6 : 7));
+  // Lower bounds of the held count at a compaction: needs_compaction() holds
+  // n > NEEDS_MIN, and wants_compaction() n > WANTS_MIN for every top_k >= 1.
+  static constexpr int NEEDS_MIN = C - 2 * kWave;
+  static constexpr int WANTS_MIN = ((kWave + 1 < CMAX ? kWave + 1 : CMAX) + C - 2 * kWave) / 2;
 
-  // Keys counted per lane in VALU, then summed over the wave with one ballot
-  // per count bit.
+  // Keys counted one 64-key row at a time: a compare into a lane mask and a
+  // scalar popcount (one VALU instruction per row).
   __device__ __forceinline__ static int count_hi_ge(const uint64_t (&v)[E], uint32_t h) {
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) c += key_hi(v[j]) >= h ? 1 : 0;
-    return wave_count_sum<EBITS>(c);
+    for (int j = 0; j < E; ++j) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key_hi(v[j]) >= h));
+    return c;
   }
 
   __device__ __forceinline__ static int count_ge(const uint64_t (&v)[E], uint64_t p) {
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) c += v[j] >= p ? 1 : 0;
-    return wave_count_sum<EBITS>(c);
+    for (int j = 0; j < E; ++j) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(v[j] >= p));
+    return c;
   }
 
   // Raises the floor so that kk <= n <= cmax (needs n > cmax and kk <= cmax).
+  // MINN is a lower bound of n known at the call: the rows below it are
+  // loaded without the per-slot check against n.
+  template <int MINN>
   __device__ __forceinline__ void compact_to(int lane, int kk, int cmax) {
+    constexpr int FULL = (MINN + 1) / kWave < E ? (MINN + 1) / kWave : E;  // rows wholly below n
     wave_lds_sync();
     uint64_t v[E];
     uint32_t mx = 0;
@@ -253,7 +259,7 @@ struct WaveSelect {
     for (int j = 0; j < E; ++j) {
       const int pos = j * kWave + lane;
       const uint64_t x = buf[pos];
-      v[j] = pos < n ? x : 0ull;
+      v[j] = (j < FULL || pos < n) ? x : 0ull;
       mx = key_hi(v[j]) > mx ? key_hi(v[j]) : mx;
     }
     mx = wave_max_u32(mx);
@@ -308,18 +314,18 @@ struct WaveSelect {
       }
     }
     wave_lds_sync();
-    int keep_l = 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) keep_l += v[j] >= P ? 1 : 0;
-    const int kbase = wave_incl_scan(keep_l, lane) - keep_l;
-    const int dbase = c + lane * E - kbase;
-    int kept = 0;
+    // The kept keys (every key >= P; P > 0, so no empty slot) are written
+    // densely, row by row in lane order; the others are not written.  r ends
+    // equal to c.
+    int r = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
       const bool keep = v[j] >= P;
-      buf[keep ? kbase + kept : dbase + (j - kept)] = v[j];
-      kept += keep ? 1 : 0;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(keep);
+      if (keep) buf[r + lanes_below(m)] = v[j];
+      r += __builtin_popcountll(m);
     }
+    (void)lane;
     n = __builtin_amdgcn_readfirstlane(c);
     floor_key = P;
     tau = __builtin_amdgcn_readfirstlane(key_hi(P));
@@ -327,7 +333,10 @@ struct WaveSelect {
   }
 
   // Keeping close to top_k keys leaves the most room and the highest floor.
-  __device__ __forceinline__ void compact(int lane) { compact_to(lane, top_k, compact_cmax()); }
+  // MINN: a lower bound of n at the call (WANTS_MIN covers every caller;
+  // NEEDS_MIN those that compact only when needs_compaction() holds).
+  template <int MINN = WANTS_MIN>
+  __device__ __forceinline__ void compact(int lane) { compact_to<MINN>(lane, top_k, compact_cmax()); }
 
   // Sorted top_k of the row, written through `out` (see TopkRowOut).  The
   // held keys are cut to exactly top_k when more are held than the sort
@@ -366,7 +375,7 @@ struct WaveSelect {
 
   template <int SE>
   __device__ __forceinline__ void finish_sorted(const TopkRowOut& out, int lane) {
-    if (n > SE * kWave) compact_to(lane, top_k, top_k);
+    if (n > SE * kWave) compact_to<SE * kWave>(lane, top_k, top_k);
     wave_lds_sync();
     uint64_t v[SE];
 #pragma unroll
@@ -402,7 +411,7 @@ struct WaveSelect {
 
   __device__ __forceinline__ void finish_merged(const TopkRowOut& out, int lane) {
     constexpr int L = 32 * kWave;  // run length
-    if (n > top_k) compact_to(lane, top_k, top_k);
+    if (n > top_k) compact_to<32 * kWave>(lane, top_k, top_k);  // (top_k > 2048 here)
     wave_lds_sync();
     sort_run(0, lane);
     sort_run(L, lane);
