@@ -144,10 +144,12 @@ struct QuantQuery {
           acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mb][ks], kb[nb][ks],
                                                                          ks == 0 ? f32x16{} : acc[nb][mb], 4, 0, 0,
                                                                          qe[mb][ks], 0, 127);
-    p0 = 0.f;
+    // (no "0 +" first term: the epilogue sums start from +0 and are never -0)
+    p0 = epilogue(acc[0][0], 0);
     p1 = 0.f;
+    if constexpr (NBLK > 1) p1 = epilogue(acc[1][0], 0);
 #pragma unroll
-    for (int mb = 0; mb < HB; ++mb) {
+    for (int mb = 1; mb < HB; ++mb) {
       p0 += epilogue(acc[0][mb], mb);
       if constexpr (NBLK > 1) p1 += epilogue(acc[1][mb], mb);
     }
@@ -173,8 +175,10 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
   static_assert(NB == 2, "one 64-key offer per tile");
   constexpr int TILE_BYTES = TILE_N * D;  // fp8 rows
   constexpr int RING = 2;
-  __shared__ __attribute__((aligned(16))) char lds[RING * TILE_BYTES + NW * C * 8];
+  // K ring, selection buffers, then the key scales of the ring's tiles.
+  __shared__ __attribute__((aligned(16))) char lds[RING * TILE_BYTES + NW * C * 8 + RING * TILE_N * 4];
   uint64_t* const sel_base = reinterpret_cast<uint64_t*>(lds + RING * TILE_BYTES);
+  float* const ksc_lds = reinterpret_cast<float*>(lds + RING * TILE_BYTES + NW * C * 8);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -213,29 +217,45 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
   KTileLoader<D / 2, TILE_N, NT> ld;
   ld.init(kst16);
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
-  if (ntiles > 0) ld.issue(kb16, kst16, 0, a.T, lds);
+  // The 64 key scales of tile t go to ksc_lds[t % 2] with one 4-byte
+  // global_load_lds by wave t % 4 (every row of the workgroup reads the same
+  // scales, and the issuing wave rotates so no SIMD does all the address
+  // work); keys past T (only in the tile that crosses T) read the last key's.
+  // Per-lane element offsets from the tile's first key: lane for a tile
+  // inside [0, T), clamped to T - 1 for the one tile that crosses T.
+  const int tcross = a.T / TILE_N;
+  const int64_t koff_l = static_cast<int64_t>(lane) * a.kcst;
+  const int64_t koff_c =
+      static_cast<int64_t>(tcross * TILE_N + lane < a.T ? lane : a.T - 1 - tcross * TILE_N) * a.kcst;
+  auto issue_scales = [&](int t) {
+    if (wave != (t & (NW - 1))) return;
+    const float* base = kscb + static_cast<int64_t>(t) * TILE_N * a.kcst;
+    const int64_t off = t == tcross ? koff_c : koff_l;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(base + off),
+                                     (lds_void*)(ksc_lds + (t & 1) * TILE_N), 4, 0, 0);
+  };
+  if (ntiles > 0) {
+    ld.issue(kb16, kst16, 0, a.T, lds);
+    issue_scales(0);
+  }
   wait_vm_lgkm0<0>();
   __syncthreads();
-
-  // Scale of this lane's key in the current tile: a pointer advanced by one
-  // tile per step (one 64-bit add instead of a multiply); keys past T (only in
-  // the tile that crosses T) read the last key's scale, as before.
-  const float* ksp = kscb + static_cast<int64_t>(okey) * a.kcst;
-  const int64_t kstep = static_cast<int64_t>(TILE_N) * a.kcst;
   // One tile; SLOT (the ring slot of tile it) is a compile-time constant, so
   // every LDS address of the tile is a per-lane base plus an immediate.
   auto tile_step = [&](const int it, auto SLOTC) {
     constexpr int slot = decltype(SLOTC)::value;
     const int tbase = it * TILE_N;
     const int t = tbase + okey;
-    // per-lane loads of this tile (the key's scale and mask byte) first, so the
-    // waits below cover the tile copies after them
-    const float kscale = *(t < a.T ? ksp : kscb + static_cast<int64_t>(a.T - 1) * a.kcst);  // (always a valid address)
-    ksp += kstep;
+    // the key's scale (LDS, before the copies below so it does not wait for
+    // them) and mask byte first
+    const float kscale = ksc_lds[slot * TILE_N + okey];
     bool mok = true;
     if constexpr (MASKED) mok = t < my_lim ? mrow[static_cast<int64_t>(t) * a.mst] != 0 : false;
     const bool more = it + 1 < ntiles;
-    if (more) ld.issue(kb16, kst16, (it + 1) * TILE_N, a.T, lds + (1 - slot) * TILE_BYTES);
+    if (more) {
+      ld.issue(kb16, kst16, (it + 1) * TILE_N, a.T, lds + (1 - slot) * TILE_BYTES);
+      issue_scales(it + 1);
+    }
     const char* tile = lds + slot * TILE_BYTES;
     int nblk = (my_lim - tbase + 31) / 32;
     nblk = nblk > NB ? NB : (nblk < 0 ? 0 : nblk);
@@ -247,7 +267,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
       const float sum = (__uint_as_float(r.x) + __uint_as_float(r.y)) * kscale;
       const bool legal = t < my_lim && mok;
       const uint64_t key = make_key(sum, static_cast<uint32_t>(t));
-      sel.offer64(legal && key_hi(key) > sel.tau, key, lane);
+      sel.offer64_masked(legal && key_hi(key) > sel.tau, key);
       if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
     }
     if (more) wait_vm_lgkm0<0>();

@@ -24,7 +24,9 @@ constexpr int kWave = 64;
 __device__ __forceinline__ uint32_t f32_to_ord(float x) {
   x = x + 0.0f;  // -0.0 + 0.0 == +0.0 under round-to-nearest
   const uint32_t b = __float_as_uint(x);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  // negative: ~b; otherwise b with the sign bit set
+  const uint32_t neg = static_cast<uint32_t>(static_cast<int32_t>(b) >> 31);
+  return b ^ (neg | 0x80000000u);
 }
 
 __device__ __forceinline__ float ord_to_f32(uint32_t o) {

@@ -215,6 +215,16 @@ struct WaveSelect {
     n = __builtin_amdgcn_readfirstlane(n + tot);
   }
 
+  // As offer64, but only the lanes with `pass` set store (an EXEC-masked
+  // store), so the other lanes' positions need no arithmetic.  For callers
+  // whose offer is not interleaved with MFMA work (the branch splits the
+  // instruction schedule).  Needs n <= C-64.
+  __device__ __forceinline__ void offer64_masked(bool pass, uint64_t key) {
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(pass);
+    if (pass) buf[n + lanes_below(bal)] = key;
+    n = __builtin_amdgcn_readfirstlane(n + __builtin_popcountll(bal));
+  }
+
   // Compacting whenever more than C - 128 keys are held leaves room for two
   // 64-key offers before the next check.
   __device__ __forceinline__ bool needs_compaction() const { return n > C - 2 * kWave; }
