@@ -445,11 +445,13 @@ void indexer_topk_kernel(IndexerArgs a) {
                                                             0, 0, 0);
           if constexpr (last_use) kf[ks] = *reinterpret_cast<const bf16x8*>(tile + boff[ks] + BLK_BYTES);
         }
+        // (the first group of each block starts its sum instead of adding to
+        // 0: an epilogue sum starts from +0 and is never -0, so 0 + e == e)
         if constexpr (ph < LAG) {
-          p1 += e;  // previous tile, block 1
+          if constexpr (ph == 0) p1 = e; else p1 += e;  // previous tile, block 1
           if constexpr (ph == LAG - 1) offer_tile(prev_p0, p1, prev_tbase, pend, prev_mask);
         } else {
-          p0 += e;  // this tile, block 0
+          if constexpr (ph == LAG) p0 = e; else p0 += e;  // this tile, block 0
         }
         // Interleave: one MFMA, then a share of the epilogue / offer VALU work.
 #pragma unroll
