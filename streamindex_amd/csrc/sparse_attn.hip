@@ -292,20 +292,30 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
         for (int mb = 0; mb < 2; ++mb)
   #pragma unroll
           for (int r = 0; r < 4; ++r) x[mb][r] = __builtin_fmaf(st[mb][r], a.scale_log2, bias[mb][r]);
-        // tile maximum: in-lane, then over the lane groups g ^ 1 and g ^ 2
-        float tmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0][0], x[0][1]), __builtin_fmaxf(x[0][2], x[0][3])),
-                                     __builtin_fmaxf(__builtin_fmaxf(x[1][0], x[1][1]), __builtin_fmaxf(x[1][2], x[1][3])));
-        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-        const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
-        tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+        // this lane's share of the tile maximum (its 8 keys)
+        const float lmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0][0], x[0][1]), __builtin_fmaxf(x[0][2], x[0][3])),
+                                           __builtin_fmaxf(__builtin_fmaxf(x[1][0], x[1][1]), __builtin_fmaxf(x[1][2], x[1][3])));
         // First valid key of the head: the accumulator and denominator are
         // still zero, so the reference moves without a rescale (alpha = 1).
         const bool first = m_ref == -1.0e30f;
-        const bool raise = first ? tmax > m_ref : tmax > m_ref + (F16 ? kLazyRescaleF16 : kLazyRescale);
-        const float m_new = raise ? tmax : m_ref;
-        out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
-        m_ref = m_new;
+        const float lazy = F16 ? kLazyRescaleF16 : kLazyRescale;
+        // A head's reference moves iff one of its four lanes' keys lifts it, so
+        // when no lane of the wave does (every tile after a head's first valid
+        // one, in practice) the reference stays and the tile maximum over the
+        // lane groups is not needed: the exponentials below use m_ref as is.
+        const bool lift = first ? lmax > m_ref : lmax > m_ref + lazy;
+        out.alpha = 1.0f;
+        if (__builtin_amdgcn_ballot_w64(lift) != 0) {
+          // tile maximum over the lane groups g ^ 1 and g ^ 2
+          const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(lmax), __float_as_uint(lmax), false, false);
+          float tmax = __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+          const SwapPair r32 = permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax));
+          tmax = __builtin_fmaxf(__uint_as_float(r32.x), __uint_as_float(r32.y));
+          const bool raise = first ? tmax > m_ref : tmax > m_ref + lazy;
+          const float m_new = raise ? tmax : m_ref;
+          out.alpha = (raise && !first) ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.0f;
+          m_ref = m_new;
+        }
         f32x2 p[4];
   #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
