@@ -100,6 +100,34 @@ def test_compacting_rows(cuda_device, top_k):
     _check(q4, qs, k8, ks, w, top_k, idx, sc, ratio=2, rows=rows, label=f"q-compact-{top_k}")
 
 
+@pytest.mark.parametrize("zero_q", [False, True])
+def test_mass_ties_through_compactions(cuda_device, zero_q):
+    # 6,000 keys made of 7 distinct rows repeated (identical fp8 rows and
+    # scales): every score is shared by ~857 keys, so the compactions set their
+    # floors by the 64-bit (score, index) bisection; with q = 0 every score is
+    # +0 and the picks are the top_k smallest indices.  Exact order against the
+    # dequantised-input oracle (score desc, index asc).
+    B, S, T, H, top_k = 1, 24, 6000, 64, 512
+    g = torch.Generator().manual_seed(4242)
+    base = torch.randn(7, 128, generator=g).to(torch.bfloat16)
+    k = base.repeat(T // 7 + 1, 1)[:T].unsqueeze(0).cuda()
+    q = torch.randn(B, S, H, 128, generator=g).to(torch.bfloat16)
+    if zero_q:
+        q.zero_()
+    q = q.cuda()
+    w = torch.randn(B, S, H, generator=g).cuda()
+    q4, qs = quant.fp4_act_quant(q, 32)
+    k8, ks = quant.act_quant(k, 128)
+    idx, sc = indexer_topk_q(q4, qs, k8, ks, w, top_k)
+    torch.cuda.synchronize()
+    qb, kb = _dequant_bits(q4, qs, k8)
+    ref = O.indexer_scores(qb[0], kb[0], w[0].cpu().numpy(), np.arange(S)) * ks.reshape(B, T).cpu().numpy()[0][None, :]
+    ridx, _ = O.topk(ref, np.full(S, T, dtype=np.int64), top_k)
+    assert np.array_equal(idx[0].cpu().numpy(), ridx)
+    if zero_q:
+        assert np.array_equal(ridx, np.tile(np.arange(top_k), (S, 1)))
+
+
 def test_quantising_wrapper_and_validation(cuda_device):
     B, S, T, H = 1, 256, 64, 64
     q, k, w, q4, qs, k8, ks = _inputs(B, S, T, H, 3)

@@ -143,6 +143,36 @@ def test_auto_picks_by_row_length(modes):
     _same(auto, b, "auto vs wide")
 
 
+@pytest.mark.parametrize("top_k,zero_q", [(100, False), (512, False), (1100, False), (512, True)])
+def test_mass_ties_through_compactions(modes, top_k, zero_q):
+    # 6,000 keys made of 7 distinct rows repeated: every score is shared by ~857
+    # keys, so a compaction's count on the score word jumps by hundreds, past
+    # every window, and the 64-bit (score, index) bisection sets the floor; with q = 0 every score is
+    # +0 and the picks are the top_k smallest indices.  Both kernels, against
+    # the oracle's (score desc, index asc) order.
+    import numpy as np
+
+    from oracle import oracle as O
+    from tests.conftest import bf16_bits
+
+    S, H, D, T = 24, 64, 128, 6000
+    g = torch.Generator().manual_seed(777 + top_k)
+    base = torch.randn(7, D, generator=g).to(torch.bfloat16)
+    k = base.repeat(T // 7 + 1, 1)[:T].unsqueeze(0).cuda()
+    q = torch.randn(1, S, H, D, generator=g).to(torch.bfloat16)
+    if zero_q:
+        q.zero_()
+    q = q.cuda()
+    w = torch.randn(1, S, H, generator=g).cuda()
+    a, b = _both(lambda: chunked_indexer_topk(q, k, w, top_k))
+    _same(a, b, f"mass ties k={top_k}")
+    ref = O.indexer_scores(bf16_bits(q[0]), bf16_bits(k[0]), w[0].cpu().numpy(), np.arange(S))
+    ridx, _ = O.topk(ref, np.full(S, T, dtype=np.int64), top_k)
+    assert np.array_equal(a[0][0].cpu().numpy(), ridx)
+    if zero_q:
+        assert np.array_equal(ridx, np.tile(np.arange(top_k), (S, 1)))
+
+
 def test_config2_full_size_kernels_agree(modes):
     # BASELINE config[2] (S=262,144, T=65,536, k=512): the automatic choice runs the
     # four-M-block kernel here; the two kernels agree on every one of the 134M outputs.
