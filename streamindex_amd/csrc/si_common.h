@@ -48,17 +48,8 @@ __device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~static_cast<ui
 // ---------------------------------------------------------------------------
 // Cross-lane helpers (ds_bpermute based; works for any xor mask in a wave64).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int lane, int mask) {
-  return static_cast<uint32_t>(
-      __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, static_cast<int>(v)));
-}
 __device__ __forceinline__ float shfl_xor_f32(float v, int lane, int mask) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
-}
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int mask) {
-  const uint32_t lo = shfl_xor_u32(static_cast<uint32_t>(v), lane, mask);
-  const uint32_t hi = shfl_xor_u32(static_cast<uint32_t>(v >> 32), lane, mask);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
@@ -130,44 +121,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
   return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
 }
 
-// Sum over the wave of a per-lane count x in [0, 2^BITS), returned
-// uniformly: one ballot per bit instead of one per counted item.
-template <int BITS>
-__device__ __forceinline__ int wave_count_sum(int x) {
-  int s = 0;
-#pragma unroll
-  for (int b = 0; b < BITS; ++b) s += __builtin_popcountll(__ballot((x >> b) & 1)) << b;
-  return s;
-}
-
-// Inclusive prefix sum over the lanes: Hillis-Steele over each 16-lane row
-// with DPP row shifts, then the totals of the lower rows added from lanes
-// 15, 31 and 47.
-__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
-  const int r0 = __builtin_amdgcn_readlane(x, 15);
-  const int r1 = __builtin_amdgcn_readlane(x, 31);
-  const int r2 = __builtin_amdgcn_readlane(x, 47);
-  const int row = lane >> 4;
-  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
-}
-
 // Number of set bits of `m` in lanes strictly below this lane.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-}
-
-// Exclusive prefix sum over the lanes of a per-lane count x in [0, 2^BITS).
-template <int BITS>
-__device__ __forceinline__ int wave_count_excl(int x) {
-  int s = 0;
-#pragma unroll
-  for (int b = 0; b < BITS; ++b) s += lanes_below(__ballot((x >> b) & 1)) << b;
-  return s;
 }
 
 // Orders this wave's LDS traffic: every LDS write issued before the call is

@@ -335,7 +335,6 @@ struct WaveSelect {
       if (keep) buf[r + lanes_below(m)] = v[j];
       r += __builtin_popcountll(m);
     }
-    (void)lane;
     n = __builtin_amdgcn_readfirstlane(c);
     floor_key = P;
     tau = __builtin_amdgcn_readfirstlane(key_hi(P));
