@@ -221,27 +221,26 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
   constexpr int OFFER_PARTS = 4;
   float osum = 0.f;     // the score of the key this lane offers
   uint64_t okey64 = 0;  // the key itself
-  bool opass = false;   // whether it passes the row's floor
+  uint64_t obal = 0;    // the lanes whose keys pass the row's floor
   int opos = 0, otot = 0;
   auto offer_part = [&](auto RC, auto PC, int tbase, bool valid, bool mok) {
     constexpr int r = decltype(RC)::value;
     constexpr int part = decltype(PC)::value;
     if constexpr (part == 0) {
       const SwapPair sp = permlane32_swap(__float_as_uint(ps[r][0]), __float_as_uint(ps[r][1]));
-      ps[r][0] = 0.f;
-      ps[r][1] = 0.f;
       osum = __uint_as_float(sp.x) + __uint_as_float(sp.y);
       pin_vgpr(osum);
     } else if constexpr (part == 1) {
       const int t = tbase + okey;
       okey64 = make_key(osum, static_cast<uint32_t>(t));
-      opass = valid && t < lim[r] && mok && key_hi(okey64) > sel[r].tau;
+      // (kept as a lane mask, not a per-lane bool, so that no 0/1 register
+      // is made and compared back)
+      obal = __builtin_amdgcn_ballot_w64(valid && t < lim[r] && mok && key_hi(okey64) > sel[r].tau);
       pin_vgpr(okey64);
     } else if constexpr (part == 2) {
-      const uint64_t bal = ballot64(opass);
-      const int below = lanes_below(bal);
-      otot = __builtin_popcountll(bal);
-      opos = opass ? sel[r].n + below : sel[r].n + otot + (lane - below);
+      const int below = lanes_below(obal);
+      otot = __builtin_popcountll(obal);
+      opos = __builtin_amdgcn_inverse_ballot_w64(obal) ? sel[r].n + below : sel[r].n + otot + (lane - below);
       pin_vgpr(opos);
     } else {
       sel[r].buf[opos] = okey64;
@@ -332,8 +331,11 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       };
       static_for<KS>(chunk);
-      // Same association as weighted_relu_sum and QueryFrags::epilogue.
-      ps[erow][enb] += s0 + s1;
+      // Same association as weighted_relu_sum and QueryFrags::epilogue.  A
+      // row's first M-block of a key block starts the partial sum (the row's
+      // offer has read the previous tile's by then; an epilogue sum starts
+      // from +0 and is never -0, so this equals adding it to zero).
+      if constexpr (emb % HB == 0) ps[erow][enb] = s0 + s1; else ps[erow][enb] += s0 + s1;
       pin_vgpr(ps[erow][enb]);
 
       if constexpr (g == MB - 1) {
@@ -382,7 +384,8 @@ void indexer_topk_wide_kernel(IndexerArgs a) {
     static_for<LAG>([&](auto GC) {
       constexpr int eg = G - LAG + decltype(GC)::value;
       constexpr int emb = eg % MB;
-      ps[emb / HB][eg / MB] += weighted_relu_sum(acc[eg % NACC], wf[emb]);
+      const float e = weighted_relu_sum(acc[eg % NACC], wf[emb]);
+      if constexpr (emb % HB == 0) ps[emb / HB][eg / MB] = e; else ps[emb / HB][eg / MB] += e;
     });
     static_for<RPW>([&](auto RC) {
       constexpr int r = decltype(RC)::value;
