@@ -373,9 +373,10 @@ void indexer_topk_kernel(IndexerArgs a) {
     const SwapPair r = permlane32_swap(__float_as_uint(p0), __float_as_uint(p1));
     const float sum = __uint_as_float(r.x) + __uint_as_float(r.y);
     const int t = tbase + okey;
-    const bool legal = valid && t < my_lim && mok;
     const uint64_t key = make_key(sum, static_cast<uint32_t>(t));
-    sel.offer64(legal && key_hi(key) > sel.tau, key, lane);
+    uint64_t bal = __builtin_amdgcn_ballot_w64(t < my_lim) & __builtin_amdgcn_ballot_w64(key_hi(key) > sel.tau);
+    if constexpr (MASKED) bal &= __builtin_amdgcn_ballot_w64(mok);
+    sel.offer64_bal(valid ? bal : 0ull, key, lane);
   };
   // Epilogues of the pending block-1 groups of the previous tile, then its offer.
   auto drain = [&]() {

@@ -105,13 +105,17 @@ struct QuantQuery {
     }
   }
 
-  __device__ __forceinline__ float epilogue(const f32x16& acc, int mb) const {
+  // Sum over this lane's 16 heads of every head block of one key block,
+  // sum_h w_h relu(acc_h) (ReLU as one v_med3_f32), as two fma chains.
+  __device__ __forceinline__ float epilogue2(const f32x16 (&acc)[HB]) const {
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      s0 = __builtin_fmaf(wf[mb][v], __builtin_amdgcn_fmed3f(acc[v], 0.f, __FLT_MAX__), s0);
-      s1 = __builtin_fmaf(wf[mb][v + 1], __builtin_amdgcn_fmed3f(acc[v + 1], 0.f, __FLT_MAX__), s1);
-    }
+    for (int mb = 0; mb < HB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        s0 = __builtin_fmaf(wf[mb][v], __builtin_amdgcn_fmed3f(acc[mb][v], 0.f, __FLT_MAX__), s0);
+        s1 = __builtin_fmaf(wf[mb][v + 1], __builtin_amdgcn_fmed3f(acc[mb][v + 1], 0.f, __FLT_MAX__), s1);
+      }
     return s0 + s1;
   }
 
@@ -144,15 +148,12 @@ struct QuantQuery {
           acc[nb][mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qa[mb][ks], kb[nb][ks],
                                                                          ks == 0 ? f32x16{} : acc[nb][mb], 4, 0, 0,
                                                                          qe[mb][ks], 0, 127);
-    // (no "0 +" first term: the epilogue sums start from +0 and are never -0)
-    p0 = epilogue(acc[0][0], 0);
+    // Two fma chains per key block run through all head blocks and are added
+    // once (one add per key block instead of one per head block and one per
+    // combination).
+    p0 = epilogue2(acc[0]);
     p1 = 0.f;
-    if constexpr (NBLK > 1) p1 = epilogue(acc[1][0], 0);
-#pragma unroll
-    for (int mb = 1; mb < HB; ++mb) {
-      p0 += epilogue(acc[0][mb], mb);
-      if constexpr (NBLK > 1) p1 += epilogue(acc[1][mb], mb);
-    }
+    if constexpr (NBLK > 1) p1 = epilogue2(acc[1]);
   }
 };
 
@@ -204,6 +205,8 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
 
   const int oblk = static_cast<int>(permlane32_swap(0u, 1u).x);
   const int okey = oblk * 32 + (lane & 31);
+  const int lim_o = my_lim - okey;                        // the key of a tile is legal iff tbase < lim_o
+  const uint32_t nokey = ~static_cast<uint32_t>(okey);    // ~(tbase + okey) == nokey - tbase
 
   WaveSelect<C> sel;
   sel.init(sel_base + wave * C, a.top_k);
@@ -245,7 +248,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
   auto tile_step = [&](const int it, auto SLOTC) {
     constexpr int slot = decltype(SLOTC)::value;
     const int tbase = it * TILE_N;
-    const int t = tbase + okey;
+    const int t = tbase + okey;  // (t < my_lim is tbase < lim_o; ~t is nokey - tbase)
     // the key's scale (LDS, before the copies below so it does not wait for
     // them) and mask byte first
     const float kscale = ksc_lds[slot * TILE_N + okey];
@@ -265,9 +268,10 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
       else qry.template tile_scores<1>(tile, lane, p0, p1);
       const SwapPair r = permlane32_swap(__float_as_uint(p0), __float_as_uint(p1));
       const float sum = (__uint_as_float(r.x) + __uint_as_float(r.y)) * kscale;
-      const bool legal = t < my_lim && mok;
-      const uint64_t key = make_key(sum, static_cast<uint32_t>(t));
-      sel.offer64_masked(legal && key_hi(key) > sel.tau, key);
+      const uint64_t key = make_key_inv(sum, nokey - static_cast<uint32_t>(tbase));
+      uint64_t bal = __builtin_amdgcn_ballot_w64(tbase < lim_o) & __builtin_amdgcn_ballot_w64(key_hi(key) > sel.tau);
+      if constexpr (MASKED) bal &= __builtin_amdgcn_ballot_w64(mok);
+      sel.offer64_masked(bal, key);
       if (sel.needs_compaction()) sel.template compact<WaveSelect<C>::NEEDS_MIN>(lane);
     }
     if (more) wait_vm_lgkm0<0>();

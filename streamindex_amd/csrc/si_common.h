@@ -42,6 +42,10 @@ __device__ __forceinline__ float ord_to_f32(uint32_t o) {
 __device__ __forceinline__ uint64_t make_key(float score, uint32_t idx) {
   return (static_cast<uint64_t>(f32_to_ord(score)) << 32) | static_cast<uint64_t>(~idx);
 }
+// make_key with the index already complemented (inv_idx = ~idx).
+__device__ __forceinline__ uint64_t make_key_inv(float score, uint32_t inv_idx) {
+  return (static_cast<uint64_t>(f32_to_ord(score)) << 32) | static_cast<uint64_t>(inv_idx);
+}
 __device__ __forceinline__ uint32_t key_hi(uint64_t k) { return static_cast<uint32_t>(k >> 32); }
 __device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~static_cast<uint32_t>(k); }
 

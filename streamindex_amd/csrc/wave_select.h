@@ -215,13 +215,25 @@ struct WaveSelect {
     n = __builtin_amdgcn_readfirstlane(n + tot);
   }
 
-  // As offer64, but only the lanes with `pass` set store (an EXEC-masked
-  // store), so the other lanes' positions need no arithmetic.  For callers
-  // whose offer is not interleaved with MFMA work (the branch splits the
-  // instruction schedule).  Needs n <= C-64.
-  __device__ __forceinline__ void offer64_masked(bool pass, uint64_t key) {
-    const uint64_t bal = __builtin_amdgcn_ballot_w64(pass);
-    if (pass) buf[n + lanes_below(bal)] = key;
+  // offer64 with the passing lanes given as a lane mask (see offer64_masked
+  // for why a mask): the branch-free append, for offers interleaved with MFMA
+  // work.  Needs n <= C-64.
+  __device__ __forceinline__ void offer64_bal(uint64_t bal, uint64_t key, int lane) {
+    const int below = lanes_below(bal);
+    const int tot = __builtin_popcountll(bal);
+    const int pos = __builtin_amdgcn_inverse_ballot_w64(bal) ? n + below : n + tot + (lane - below);
+    buf[pos] = key;
+    n = __builtin_amdgcn_readfirstlane(n + tot);
+  }
+
+  // As offer64 for the lanes set in the lane mask `bal`, but only those lanes
+  // store (an EXEC-masked store), so the other lanes' positions need no
+  // arithmetic.  For callers whose offer is not interleaved with MFMA work
+  // (the branch splits the instruction schedule).  The caller forms `bal` as
+  // an AND of ballots of single compares: a ballot of a combined condition
+  // makes the compiler rebuild the mask from a 0/1 register.  Needs n <= C-64.
+  __device__ __forceinline__ void offer64_masked(uint64_t bal, uint64_t key) {
+    if (__builtin_amdgcn_inverse_ballot_w64(bal)) buf[n + lanes_below(bal)] = key;
     n = __builtin_amdgcn_readfirstlane(n + __builtin_popcountll(bal));
   }
 
