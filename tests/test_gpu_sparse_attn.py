@@ -94,6 +94,33 @@ def test_masking_equals_truncation(cuda_device):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+@pytest.mark.parametrize("D", [576, 128])
+def test_reference_maximum_jumps(cuda_device, D):
+    # Scores that rise by far more than the lazy threshold (2^64 in exp2 units)
+    # in later tiles, twice: the softmax takes the path that reduces the tile
+    # maximum over the lane groups, moves the reference and rescales the
+    # accumulated output (alpha < 1) mid-row; the first tiles keep it fixed.
+    B, S, H, N, K = 1, 6, 64, 320, 320
+    g = torch.Generator().manual_seed(211 + D)
+    u = torch.randn(D, generator=g) * 10.0
+    q = (u + torch.randn(B, S, H, D, generator=g)).to(torch.bfloat16)
+    kv = (torch.randn(B, N, D, generator=g) * 0.01)
+    scale = D ** -0.5
+    # key rows 256..287 score about 80 / scale (115 in exp2 units, past the
+    # threshold of 64 over the cold keys' ~0), rows 288..319 about 200 / scale
+    # (288: past it again); outputs stay below 8, where bf16 rounds by <= 2^-6
+    kv[0, 256:288] = u * (80.0 / scale) / u.dot(u)
+    kv[0, 288:320] = u * (200.0 / scale) / u.dot(u)
+    kv = kv.to(torch.bfloat16)
+    sink = torch.randn(H, generator=g)
+    idx = torch.arange(K, dtype=torch.int32).repeat(B, S, 1)  # hot keys in tiles 8 and 9
+    q, kv, sink, idx = q.cuda(), kv.cuda(), sink.cuda(), idx.cuda()
+    o, lse = sparse_attn_fwd(q, kv, sink, idx, scale)
+    torch.cuda.synchronize()
+    _check(q, kv, sink, idx, scale, o, lse, label=f"jumps D={D}")
+    assert float(lse.min()) > 100.0  # the hot keys dominate every head
+
+
 @pytest.mark.parametrize("D,i64", [(576, False), (128, True), (512, False)])
 def test_fully_masked_tiles(cuda_device, D, i64):
     # Whole 32-key tiles of -1 (the first tile, tiles in the middle, the last
