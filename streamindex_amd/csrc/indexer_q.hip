@@ -13,9 +13,9 @@
 // and since scale(t) > 0, I(s, t) = scale(t) sum_h w relu(q . k_e4m3): the key
 // scale multiplies the finished score.
 //
-// Design: one query row per wavefront, four rows per workgroup, 64-key tiles
-// of fp8 rows (D bytes each) copied HBM/L2 -> LDS by global_load_lds into a
-// double-buffered swizzled ring (the bf16 kernel's loader, a fp8 row of D
+// Design: one query row per wavefront, four or eight rows per workgroup
+// (TopkQShape), 64-key tiles of fp8 rows (D bytes each) copied HBM/L2 -> LDS
+// by global_load_lds into a double-buffered swizzled ring (the bf16 kernel's loader, a fp8 row of D
 // bytes being laid out like a bf16 row of D/2 elements).  One
 // v_mfma_scale_f32_32x32x64_f8f6f4 per 32 heads x 32 keys x 64 dims: the A
 // operand is the row's fp4 Q (16 bytes per lane, 32 consecutive dims) with
@@ -157,19 +157,24 @@ struct QuantQuery {
   }
 };
 
-// Launch shape: as the bf16 kernel (four rows, 64-key tiles) with up to three
-// workgroups per CU while the selection buffers leave room in LDS (the fp8
-// ring is half the bf16 one and the fragments use fewer VGPRs).
+// Launch shape: as the bf16 kernel (64-key tiles, one query row per wave)
+// with more waves per SIMD, which the fp8 ring (half the bf16 one) and the
+// smaller fragments allow.  At C = 960 (top_k <= 512) a workgroup takes
+// eight rows that share one K ring, and two such workgroups fill a CU: four
+// waves per SIMD at 128 VGPRs, 2 x 76.5 KiB of LDS (960 keys is the most
+// selection buffer that leaves two).  Otherwise four rows per workgroup and
+// three workgroups per CU while the selection buffers leave room in LDS.
 template <int C>
 struct TopkQShape {
-  static constexpr int WAVES_PER_EU = C <= 1152 ? 3 : 1;
+  static constexpr int NW = C == 960 ? 8 : 4;
+  static constexpr int WAVES_PER_EU = NW == 8 ? 4 : (C <= 1152 ? 3 : 1);
 };
 
 template <int HB, int D, int C, bool MASKED>
-__global__ __launch_bounds__(TopkShape<C>::NW * 64)
+__global__ __launch_bounds__(TopkQShape<C>::NW * 64)
 __attribute__((amdgpu_waves_per_eu(TopkQShape<C>::WAVES_PER_EU, TopkQShape<C>::WAVES_PER_EU)))
 void indexer_topk_q_kernel(IndexerQArgs a) {
-  constexpr int NW = TopkShape<C>::NW;
+  constexpr int NW = TopkQShape<C>::NW;
   constexpr int NT = NW * 64;
   constexpr int TILE_N = TopkShape<C>::TILE_N;
   constexpr int NB = TILE_N / 32;
@@ -303,7 +308,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
 template <int HB, int D, int C>
 static int launch_q(const IndexerQArgs& a, hipStream_t st) {
   if (a.top_k > WaveSelect<C>::MAX_TOPK) return set_error(SI_ERR_UNSUPPORTED, "top_k exceeds the selection capacity");
-  constexpr int NW = TopkShape<C>::NW;
+  constexpr int NW = TopkQShape<C>::NW;
   const int64_t nqb = (static_cast<int64_t>(a.S) + NW - 1) / NW;
   const int64_t grid = nqb * a.B;
   if (grid > 0x7fffffffLL) return set_error(SI_ERR_UNSUPPORTED, "grid too large");
@@ -321,6 +326,10 @@ template <int HB, int D>
 static int dispatch_q(const IndexerQArgs& a, hipStream_t st) {
   if (a.top_k <= 32) return launch_q<HB, D, 256>(a, st);
   if (a.top_k <= 192) return launch_q<HB, D, 512>(a, st);
+  // (eight rows per workgroup, four waves per SIMD: against four rows, three
+  // workgroups per CU and C = 1152, -3.8 % at S = 1M and even at 64K, where
+  // C = 896 cost 1 % in compactions)
+  if (a.top_k <= 512) return launch_q<HB, D, 960>(a, st);
   // (1152 = the most that leaves three workgroups per CU: 52 KiB of LDS each;
   // fewer compactions than 1024, measured -1.3 % at S = 64K)
   if (a.top_k <= 640) return launch_q<HB, D, 1152>(a, st);
