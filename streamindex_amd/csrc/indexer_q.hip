@@ -159,14 +159,14 @@ struct QuantQuery {
 
 // Launch shape: as the bf16 kernel (64-key tiles, one query row per wave)
 // with more waves per SIMD, which the fp8 ring (half the bf16 one) and the
-// smaller fragments allow.  At C = 960 (top_k <= 512) a workgroup takes
+// smaller fragments allow.  Up to C = 960 (top_k <= 512) a workgroup takes
 // eight rows that share one K ring, and two such workgroups fill a CU: four
-// waves per SIMD at 128 VGPRs, 2 x 76.5 KiB of LDS (960 keys is the most
-// selection buffer that leaves two).  Otherwise four rows per workgroup and
-// three workgroups per CU while the selection buffers leave room in LDS.
+// waves per SIMD at 128 VGPRs, at most 2 x 76.5 KiB of LDS (960 keys is the
+// largest selection buffer that leaves two).  Above, four rows per workgroup
+// and three workgroups per CU while the selection buffers leave room in LDS.
 template <int C>
 struct TopkQShape {
-  static constexpr int NW = C == 960 ? 8 : 4;
+  static constexpr int NW = C <= 960 ? 8 : 4;
   static constexpr int WAVES_PER_EU = NW == 8 ? 4 : (C <= 1152 ? 3 : 1);
 };
 
@@ -324,11 +324,12 @@ static int launch_q(const IndexerQArgs& a, hipStream_t st) {
 
 template <int HB, int D>
 static int dispatch_q(const IndexerQArgs& a, hipStream_t st) {
+  // (eight rows per workgroup, four waves per SIMD, against four rows and three
+  // workgroups per CU: top_k 32 -4.5 % at 64K; 128 -3.8 % at 64K, -4.3 % at
+  // S = 1M; 512 (C = 960 against C = 1152) -3.8 % at 1M and even at 64K,
+  // where C = 896 cost 1 % in compactions)
   if (a.top_k <= 32) return launch_q<HB, D, 256>(a, st);
   if (a.top_k <= 192) return launch_q<HB, D, 512>(a, st);
-  // (eight rows per workgroup, four waves per SIMD: against four rows, three
-  // workgroups per CU and C = 1152, -3.8 % at S = 1M and even at 64K, where
-  // C = 896 cost 1 % in compactions)
   if (a.top_k <= 512) return launch_q<HB, D, 960>(a, st);
   // (1152 = the most that leaves three workgroups per CU: 52 KiB of LDS each;
   // fewer compactions than 1024, measured -1.3 % at S = 64K)

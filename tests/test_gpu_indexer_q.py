@@ -88,12 +88,13 @@ def test_large_topk_sampled_rows(cuda_device):
     _check(q4, qs, k8, ks, w, 1024, idx, sc, ratio=4, rows=rows, label="q-1024")
 
 
-@pytest.mark.parametrize("top_k", [193, 512, 640])
+@pytest.mark.parametrize("top_k", [32, 192, 193, 512, 640])
 def test_compacting_rows(cuda_device, top_k):
-    # top_k in (192, 512] runs the 960-key selection buffer with eight rows per
-    # workgroup, (512, 640] the 1152-key one with four; rows of up to 4096
-    # keys compact them several times.  S = 8189 leaves the last (first
-    # scheduled) workgroup with five active rows.
+    # top_k <= 32, (32, 192] and (192, 512] run the 256-, 512- and 960-key
+    # selection buffers with eight rows per workgroup, (512, 640] the
+    # 1152-key one with four; rows of up to 4096 keys compact them several
+    # times.  S = 8189 leaves the last (first scheduled) workgroup with five
+    # active rows.
     B, S, T, H = 1, 8189, 4096, 64
     _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 31 + top_k)
     idx, sc = indexer_topk_q(q4, qs, k8, ks, w, top_k, causal_ratio=2)
