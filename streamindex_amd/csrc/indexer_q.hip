@@ -15,8 +15,9 @@
 //
 // Design: one query row per wavefront, four or eight rows per workgroup
 // (TopkQShape), 64-key tiles of fp8 rows (D bytes each) copied HBM/L2 -> LDS
-// by global_load_lds into a double-buffered swizzled ring (the bf16 kernel's loader, a fp8 row of D
-// bytes being laid out like a bf16 row of D/2 elements).  One
+// by global_load_lds into a double-buffered swizzled ring (the bf16 kernel's
+// loader, a fp8 row of D bytes being laid out like a bf16 row of D/2
+// elements).  One
 // v_mfma_scale_f32_32x32x64_f8f6f4 per 32 heads x 32 keys x 64 dims: the A
 // operand is the row's fp4 Q (16 bytes per lane, 32 consecutive dims) with
 // its E8M0 block scale per lane, the B operand two 16-byte chunks of a key
@@ -226,7 +227,7 @@ void indexer_topk_q_kernel(IndexerQArgs a) {
   ld.init(kst16);
   const int ntiles = (wg_lim + TILE_N - 1) / TILE_N;
   // The 64 key scales of tile t go to ksc_lds[t % 2] with one 4-byte
-  // global_load_lds by wave t % 4 (every row of the workgroup reads the same
+  // global_load_lds by wave t % NW (every row of the workgroup reads the same
   // scales, and the issuing wave rotates so no SIMD does all the address
   // work); keys past T (only in the tile that crosses T) read the last key's.
   // Per-lane element offsets from the tile's first key: lane for a tile
