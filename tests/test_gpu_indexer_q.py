@@ -58,7 +58,9 @@ def _inputs(B, S, T, H, seed):
 
 @pytest.mark.parametrize("H,top_k", [(64, 64), (16, 32), (40, 200)])
 def test_causal_ratio(cuda_device, H, top_k):
-    B, S, T = 2, 600, 150
+    # two batches of 603 rows: each batch's last eight-row workgroup holds
+    # three rows
+    B, S, T = 2, 603, 150
     _, _, w, q4, qs, k8, ks = _inputs(B, S, T, H, 11 + H)
     idx, sc = indexer_topk_q(q4, qs, k8, ks, w, top_k, causal_ratio=4)
     torch.cuda.synchronize()
