@@ -175,6 +175,25 @@ __device__ __forceinline__ void reg_tie(T& x) {
   asm volatile("" : "+v"(x));
 }
 
+// Block order of the forward's row groups.  Workgroups go to the 8 XCDs
+// round-robin, so consecutive blocks run on different L2s.  Within every full
+// chunk of 256 blocks this returns, for XCD x, 32 consecutive block numbers
+// instead, so
+// that queries sharing KV rows (HCA / CSA windows and compressed rows) gather
+// them through one L2, while every XCD still gets a share of each chunk (the
+// order of the chunks themselves is unchanged).  A bijection on
+// [0, gridDim.x); the partial last chunk keeps the plain order.  (The
+// backward's row kernel measured the same with it: its time is its row and
+// reduction traffic, not gather locality.)
+__device__ __forceinline__ int xcd_block_order() {
+  constexpr int kXcds = 8, kPerXcd = 32;
+  int lb = static_cast<int>(blockIdx.x);
+  const int chunk = lb / (kXcds * kPerXcd);
+  if ((chunk + 1) * (kXcds * kPerXcd) <= static_cast<int>(gridDim.x))
+    lb = chunk * (kXcds * kPerXcd) + (lb % kXcds) * kPerXcd + (lb / kXcds) % kPerXcd;
+  return lb;
+}
+
 // Tile barrier of the main loops.  __syncthreads() carries a workgroup
 // release fence, for which the compiler waits on every outstanding LDS-DMA
 // copy (vmcnt(0)) -- including the gathers just issued for later tiles, which

@@ -136,8 +136,11 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_attn_fwd_kernel(SparseAtt
   const int g = lane >> 4;     // lane group 0..3
   const int i16 = lane & 15;
   const int nsg = (a.S + kAttnRows - 1) / kAttnRows;  // row groups
-  const int sg = blockIdx.x % nsg;
-  const int rest = blockIdx.x / nsg;
+  // (XCD-aware block order, xcd_block_order: HCA attention -2.5 %, CSA
+  // attention -2 % at S = 64K, config[3]'s scattered picks unchanged)
+  const int lb = xcd_block_order();
+  const int sg = lb % nsg;
+  const int rest = lb / nsg;
   const int b = rest % a.B;
   const int hg = rest / a.B;
   const int hbase = hg * 64;
