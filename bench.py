@@ -447,6 +447,41 @@ def run_indexer_q(S, ratio, top_k, steps, warmup, H=64, D=128, seed=2026, parity
             "parity_rows": int(len(rows)), "recall_mean": float(rec.mean()), "recall_min": float(rec.min())}
 
 
+def run_indexer_score(S, steps, warmup, ratio=4, H=64, D=128, seed=2026, parity_rows=16):
+    """The materialised-score operator (`indexer_score`: every (s, t) pair, no
+    mask, as the reference kernel) at config[1]'s shape: S x T fp32 scores
+    (4 GiB at S = 64K).  Dense work 2*H*D per pair; its output writes bound it
+    below the MFMA time only for much longer rows.  Sampled rows are checked
+    against the oracle's float64 scores (the tests' 1e-4 relative gate)."""
+    from oracle import oracle as O
+    from streamindex_amd import indexer_score
+
+    dev = torch.device("cuda:0")
+    q, k, w = synth.indexer_inputs(1, S, H, D, ratio=ratio, seed=seed, device=dev)
+    T = k.shape[1]
+    fn = lambda: indexer_score(q, k, w)  # noqa: E731
+    for _ in range(max(1, warmup)):
+        out = fn()
+    del out
+    torch.cuda.synchronize()
+    ms = _events_time(fn, steps, torch.cuda.current_stream(dev))
+    sc = fn()
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(11).choice(S, size=min(parity_rows, S), replace=False)).astype(np.int64)
+    ref = O.indexer_scores(_bits(q[0]), _bits(k[0]), w[0].float().cpu().numpy(), rows)
+    got = sc[0, torch.from_numpy(rows).to(dev)].double().cpu().numpy()
+    scale = np.abs(ref).mean(axis=1, keepdims=True)
+    err = float((np.abs(got - ref) / (np.abs(ref) + scale)).max())
+    flops = 2.0 * H * D * S * T
+    out_bytes = 4.0 * S * T
+    del sc, q, k, w
+    torch.cuda.empty_cache()
+    return {"S": S, "T": T, "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "mfma_frac": flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "write_gbps": out_bytes / (ms * 1e-3) / 1e9, "output_gib": out_bytes / 2 ** 30,
+            "parity_rows": int(len(rows)), "max_rel_err": err, "pass": err < 1e-4}
+
+
 def attn_parity(q, kv, sink, idx, o, lse, nrows=64, seed=33):
     """Sampled rows of a sparse-attention output against the oracle over the
     same index rows: max |o - o_ref| (gate 2e-2) and max |lse - lse_ref|."""
@@ -746,6 +781,8 @@ def main():
     ap.add_argument("--only-indexer-q", type=int, default=0, metavar="S",
                     help="fp4/fp8 indexer timing only at sequence length S (for profilers)")
     ap.add_argument("--no-indexer-q", action="store_true", help="skip the fp4/fp8 indexer measurements")
+    ap.add_argument("--no-score", action="store_true", help="skip the materialised-score (indexer_score) leg")
+    ap.add_argument("--only-score", action="store_true", help="indexer_score timing only (for profilers)")
     ap.add_argument("--no-attn-bwd", action="store_true", help="skip the sparse-attention backward measurement")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end CSA forward measurements")
     ap.add_argument("--e2e-parity-rows", type=int, default=1024,
@@ -780,6 +817,9 @@ def main():
     if args.only_indexer_q:
         rq = run_indexer_q(args.only_indexer_q, args.ratio, args.top_k, args.steps, args.warmup)
         print(json.dumps(rq), flush=True)
+        return
+    if args.only_score:
+        print(json.dumps(run_indexer_score(65536, args.steps, args.warmup, args.ratio)), flush=True)
         return
     if args.only_attn_bwd:
         ri = run_indexer(65536, args.ratio, args.top_k, args.chunk_s, args.chunk_t, 1, 1)
@@ -897,6 +937,10 @@ def main():
         if not args.no_long:
             extra["indexer_q_s1m"] = run_indexer_q(1 << 20, args.ratio, args.top_k, 1, 1, parity_rows=64)
         torch.cuda.empty_cache()
+
+    if not args.no_score:
+        say("indexer_score (materialised scores) at config[1]'s shape")
+        extra["indexer_score_c1"] = run_indexer_score(65536, 5, 2, args.ratio)
 
     if not args.no_e2e:
         say("end-to-end CSA forward S=64K")

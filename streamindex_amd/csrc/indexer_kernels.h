@@ -183,8 +183,10 @@ struct QueryFrags {
     return s0 + s1;
   }
 
-  // Score of key (block base + lane%32) for this row; identical in lanes l and l+32.
-  __device__ __forceinline__ float score(const bf16x8 (&kb)[KS], int lane) const {
+  // This lane's half of the head sum of one 32-key block (key lane % 32,
+  // the lane's 16 heads per head block); the two halves are added across the
+  // half-waves by the caller.
+  __device__ __forceinline__ float partial(const bf16x8 (&kb)[KS]) const {
     f32x16 acc[HB];
 #pragma unroll
     for (int mb = 0; mb < HB; ++mb) acc[mb] = f32x16{};
@@ -198,22 +200,25 @@ struct QueryFrags {
     float sum = 0.f;
 #pragma unroll
     for (int mb = 0; mb < HB; ++mb) sum += epilogue(acc[mb], mb);
-    return sum + shfl_xor_f32(sum, lane, 32);
+    return sum;
   }
 
-  // Scores of the first `nblk` 32-key blocks of a tile (all NB when FULL);
-  // block nb+1's B-fragments are read while block nb's MFMAs execute.
+  // Partial head sums (partial()) of the first `nblk` 32-key blocks of a tile
+  // (all NB when FULL, 0 for the others).  One set of B-fragments at a time:
+  // a second set (reads of block nb+1 behind block nb's MFMAs) needs the 32
+  // registers whose spills, reloaded from scratch every tile, made each tile
+  // wait for the next tile's copy (vector memory completes in order); the
+  // other wave of the SIMD covers the LDS latency instead.
   template <int NB, bool FULL>
-  __device__ __forceinline__ void tile_scores(const char* tile, int nblk, int lane, float (&sc)[NB]) const {
-    bf16x8 kb[2][KS];
-    load_b(tile, 0, lane, kb[0]);
+  __device__ __forceinline__ void tile_partials(const char* tile, int nblk, int lane, float (&p)[NB]) const {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if (FULL || nb < nblk) {
-        if (nb + 1 < NB && (FULL || nb + 1 < nblk)) load_b(tile, nb + 1, lane, kb[(nb + 1) & 1]);
-        sc[nb] = score(kb[nb & 1], lane);
+        bf16x8 kb[KS];
+        load_b(tile, nb, lane, kb);
+        p[nb] = partial(kb);
       } else {
-        sc[nb] = 0.f;
+        p[nb] = 0.f;
       }
     }
   }
@@ -558,30 +563,47 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
   const int ntiles = (a.T + TILE_N - 1) / TILE_N;
   if (ntiles > 0) ld.issue(kb, a.kst, 0, a.T, lds);
   tile_barrier();
+  static_assert(NB % 2 == 0, "32-key blocks are stored in pairs");
   for (int it = 0; it < ntiles; ++it) {
     const bool more = it + 1 < ntiles;
     if (more) ld.issue(kb, a.kst, (it + 1) * TILE_N, a.T, lds + ((it + 1) & 1) * TILE_BYTES);
     const char* tile = lds + (it & 1) * TILE_BYTES;
+    const int tbase = it * TILE_N;
+    // Full tiles of a row that overwrites its scores issue exactly NB / 2
+    // stores after the copy of tile it+1, so the wait before the barrier
+    // leaves them in flight and covers only that copy (vector memory
+    // operations complete in issue order); every other case waits for all.
+    const bool lean = active && !a.accumulate && tbase + TILE_N <= a.T;
     if (active) {
-      const int tbase = it * TILE_N;
       int nblk = (a.T - tbase + 31) / 32;
       nblk = nblk > NB ? NB : nblk;
-      float sc[NB];
+      float p[NB];
       if (nblk == NB) {
-        qfr.template tile_scores<NB, true>(tile, NB, lane, sc);
+        qfr.template tile_partials<NB, true>(tile, NB, lane, p);
       } else {
-        qfr.template tile_scores<NB, false>(tile, nblk, lane, sc);
+        qfr.template tile_partials<NB, false>(tile, nblk, lane, p);
       }
+      // Blocks 2j and 2j+1: one half-wave swap leaves key 64j + lane's sum in
+      // lane `lane` (block 2j's in lanes 0-31, block 2j+1's in 32-63), so each
+      // pair is one coalesced 64-lane store.
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int t = tbase + nb * 32 + (lane & 31);
-        if (nb < nblk && lane < 32 && t < a.T) {
-          float* o = orow + static_cast<int64_t>(t) * a.sst;
-          *o = a.accumulate ? *o + sc[nb] : sc[nb];
+      for (int j = 0; j < NB / 2; ++j) {
+        const SwapPair r = permlane32_swap(__float_as_uint(p[2 * j]), __float_as_uint(p[2 * j + 1]));
+        const float v = __uint_as_float(r.x) + __uint_as_float(r.y);
+        const int t = tbase + 64 * j + lane;
+        float* o = orow + static_cast<int64_t>(t) * a.sst;
+        if (lean) {
+          *o = v;
+        } else if (t < a.T) {
+          *o = a.accumulate ? *o + v : v;
         }
       }
     }
-    tile_barrier();
+    asm volatile("" ::: "memory");
+    if (lean) wait_vm_lgkm0<NB / 2>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
 }
 

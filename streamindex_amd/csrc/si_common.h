@@ -50,12 +50,8 @@ __device__ __forceinline__ uint32_t key_hi(uint64_t k) { return static_cast<uint
 __device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~static_cast<uint32_t>(k); }
 
 // ---------------------------------------------------------------------------
-// Cross-lane helpers (ds_bpermute based; works for any xor mask in a wave64).
+// Cross-lane helpers.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float shfl_xor_f32(float v, int lane, int mask) {
-  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
-}
-
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
 // Value of lane (this lane ^ LX) for LX in {1, 2, 4, 8, 16, 32}, without LDS:
