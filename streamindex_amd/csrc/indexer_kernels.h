@@ -572,7 +572,9 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_score_kernel(IndexerArgs a
     // Full tiles of a row that overwrites its scores issue exactly NB / 2
     // stores after the copy of tile it+1, so the wait before the barrier
     // leaves them in flight and covers only that copy (vector memory
-    // operations complete in issue order); every other case waits for all.
+    // operations -- global loads, LDS-DMA copies, stores -- report completion
+    // to the wave in execution order on this GFX9-family part, which is what
+    // vmcnt counts); every other case waits for all.
     const bool lean = active && !a.accumulate && tbase + TILE_N <= a.T;
     if (active) {
       int nblk = (a.T - tbase + 31) / 32;
