@@ -707,8 +707,14 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
   const int grp = threadIdx.x / CPR;
   const int c = threadIdx.x % CPR;
   float* accp = r.acc + static_cast<int64_t>(kid) * D + c * 8;
-  // The running sum of the earlier chunks is read first, so that its load
-  // overlaps the segment's row loads instead of following them.
+  const int lo = r.seg_lo[kid], hi = r.seg_hi[kid];
+  // A key that no query of this chunk selects keeps its running sum where it
+  // is (the first chunk still writes its zeros, the last its dkv row): with
+  // window and compressed keys, most of the keys of a chunk of queries are
+  // such keys, and rewriting their sums would move 2 x 4 x D bytes each.
+  if (lo == hi && !r.first && !r.last) return;
+  // The running sum of the earlier chunks is read before the rows, so that
+  // its load overlaps the segment's row loads instead of following them.
   float prev[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (!r.first && threadIdx.x < CPR) {
     const f32x4 a0 = *reinterpret_cast<const f32x4*>(accp);
@@ -721,7 +727,6 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
   }
   float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
-    const int lo = r.seg_lo[kid], hi = r.seg_hi[kid];
     auto add_row = [&](int p) {
       const uint32_t pid = r.pair[p];
       const int64_t lrow = pid / static_cast<uint32_t>(r.K) - r.prow0;
