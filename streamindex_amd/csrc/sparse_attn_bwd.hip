@@ -743,17 +743,25 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
     int p = lo + grp;
     if (grp < G) {
       if (r.HG == 1) {
-        // one head group: 8 pair ids, then 8 independent row loads in flight
-        for (; p + 7 * G < hi; p += 8 * G) {
-          uint32_t pid[8];
+        // one head group: 8 independent row loads in flight, and the next 8
+        // pair ids loaded behind them, so that a long segment waits for one
+        // memory round trip per 8 rows instead of two
+        uint32_t pid[8];
+        if (p + 7 * G < hi) {
 #pragma unroll
           for (int u = 0; u < 8; ++u) pid[u] = r.pair[p + u * G];
+        }
+        for (; p + 7 * G < hi; p += 8 * G) {
           u32x4 v[8];
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
             const int64_t lrow = pid[u] / static_cast<uint32_t>(r.K) - r.prow0;
             const int64_t j = pid[u] % static_cast<uint32_t>(r.K);
             v[u] = *reinterpret_cast<const u32x4*>(r.prow + (lrow * r.KP + j) * D + c * 8);
+          }
+          if (p + 15 * G < hi) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) pid[u] = r.pair[p + 8 * G + u * G];
           }
 #pragma unroll
           for (int u = 0; u < 8; ++u)
