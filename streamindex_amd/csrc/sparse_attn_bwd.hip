@@ -771,6 +771,36 @@ __global__ __launch_bounds__(ReduceShape<D>::NT) void sparse_attn_bwd_dkv_reduce
               sum[2 * e + 1] += elem_hi<F16>(v[u][e]);
             }
         }
+        // The group's last (at most 7) rows as one round rather than one
+        // round trip pair each: the same rows, added in the same order.  The
+        // loads are unconditional (a slot past the segment reads the round's
+        // first row again) and a select keeps those slots out of the sums, so
+        // no branch splits the loads apart.
+        if (p < hi) {
+          const int n = (hi - p + G - 1) / G;
+          uint32_t pr[7];
+          u32x4 vr[7];
+#pragma unroll
+          for (int u = 0; u < 7; ++u) pr[u] = r.pair[u < n ? p + u * G : p];
+#pragma unroll
+          for (int u = 0; u < 7; ++u) {
+            const int64_t lrow = pr[u] / static_cast<uint32_t>(r.K) - r.prow0;
+            const int64_t j = pr[u] % static_cast<uint32_t>(r.K);
+            vr[u] = *reinterpret_cast<const u32x4*>(r.prow + (lrow * r.KP + j) * D + c * 8);
+          }
+#pragma unroll
+          for (int u = 0; u < 7; ++u) {
+            const bool in = u < n;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo_v = sum[2 * e] + elem_lo<F16>(vr[u][e]);
+              const float hi_v = sum[2 * e + 1] + elem_hi<F16>(vr[u][e]);
+              sum[2 * e] = in ? lo_v : sum[2 * e];
+              sum[2 * e + 1] = in ? hi_v : sum[2 * e + 1];
+            }
+          }
+          p = hi;
+        }
       } else {
         for (; p + 7 * G < hi; p += 8 * G) {
 #pragma unroll
